@@ -1,0 +1,169 @@
+"""Benchmark of the vocabulary-wide token path on one MI355X.
+
+A step is one pass of the hot path over the large-vocabulary workload:
+the sampler over a bf16 [256, 248320] batch (repetition penalty over a
+4096-token history, 8%-density allow mask, T 0.7, top-k 64, top-p 0.9) and
+one logprob/entropy pass over bf16 [8192, 248320] with int32 targets.
+Inputs are generated on the GPU and resident in HBM before timing; two
+sampler batches alternate so consecutive steps do not hit the 256 MB MALL
+(the 4 GB logprob pass between them evicts it as well).
+
+Prints ONE JSON line.  ``value`` is sampled rows/s of the sampler kernel;
+``logprob_tokens_per_s`` is the logprob kernel's throughput.  Kernel times
+come from HIP events around each launch on the launch stream.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+
+def cpu_baseline(wl_cpu, lx_cpu, lt_cpu):
+    """The reference's CPU path (oracle/cpu_reference.py), timed on a bounded
+    sample of the same workload with all host threads."""
+    import torch
+
+    from graspo_amd import workloads as W
+    from oracle import cpu_reference as CR
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rows = 32
+    x = wl_cpu.logits[:rows]
+    bits = W.unpack_mask(wl_cpu.allow_mask[:rows], x.shape[1])
+    kw = dict(temperature=wl_cpu.temperature, top_k=wl_cpu.top_k, top_p=wl_cpu.top_p,
+              repetition_penalty=wl_cpu.repetition_penalty, history=wl_cpu.history[:rows],
+              allow_mask_bits=bits, uniforms=wl_cpu.uniforms[:rows])
+    CR.sample_rows(x, **kw)  # warmup
+    reps, t0 = 0, time.perf_counter()
+    while reps < 5 or time.perf_counter() - t0 < 5.0:
+        CR.sample_rows(x, **kw)
+        reps += 1
+    s_rows = rows * reps / (time.perf_counter() - t0)
+    lrows = lx_cpu.shape[0]
+    CR.logprob_entropy_rows(lx_cpu, lt_cpu)
+    reps, t0 = 0, time.perf_counter()
+    while reps < 5 or time.perf_counter() - t0 < 5.0:
+        CR.logprob_entropy_rows(lx_cpu, lt_cpu)
+        reps += 1
+    l_tok = lrows * reps / (time.perf_counter() - t0)
+    return {
+        "value": round(s_rows, 2),
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"sampler: {rows} rows of the bf16 [256, 248320] batch, full V; "
+                  f"logprob: {lrows} rows of [8192, 248320] -> {l_tok:.1f} tokens/s",
+        "logprob_tokens_per_s": round(l_tok, 2),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "rows are independent, so N GPUs would each run B/N rows of the same kernels",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import graspo_amd
+    from graspo_amd import ops
+    from graspo_amd import workloads as W
+
+    graspo_amd.load()
+    dev = torch.device("cuda:0")
+    wl = W.sampler_workload(5, device=dev)
+    wl_b = W.SamplerWorkload(**{**wl.__dict__, "logits": wl.logits.clone()})
+    batches = [wl, wl_b]
+    lx, lt = W.logprob_workload(5, device=dev)
+    B, V = wl.logits.shape
+    N = lx.shape[0]
+    torch.cuda.synchronize()
+
+    def step(i, evs=None):
+        w = batches[i % 2]
+        if evs:
+            evs[0].record()
+        ops.sample(w.logits, **w.kwargs())
+        if evs:
+            evs[1].record()
+        ops.logprob_entropy(lx, lt)
+        if evs:
+            evs[2].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    s_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    l_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+
+    s_bytes = wl.algorithmic_bytes()
+    l_bytes = W.logprob_algorithmic_bytes(N, V, lx.element_size())
+    s_gbs = s_bytes / (s_ms * 1e-3) / 1e9
+    l_gbs = l_bytes / (l_ms * 1e-3) / 1e9
+    roof_s = {"bound": "hbm", "achieved": round(s_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+              "frac": round(s_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+              "kernel": "sampler_kernel<bf16>", "algorithmic_bytes": s_bytes,
+              "avg_us": round(s_ms * 1e3, 2)}
+    roof_l = {"bound": "hbm", "achieved": round(l_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+              "frac": round(l_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+              "kernel": "logprob_entropy_kernel<bf16>", "algorithmic_bytes": l_bytes,
+              "avg_us": round(l_ms * 1e3, 2)}
+    dominant = roof_l if l_ms >= s_ms else roof_s
+    line = {
+        "metric": "sampled rows/sec and logprob tokens/sec; achieved HBM GB/s vs MI355X peak",
+        "value": round(B / (s_ms * 1e-3), 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "large-vocab sampler bf16 [256,248320] (hist 4096, rho 1.05, mask 8%, "
+                        "T 0.7, top-k 64, top-p 0.9) + logprob/entropy bf16 [8192,248320]",
+            "sampler_batch": B, "vocab": V, "logprob_rows": N, "input_dtype": "bf16",
+            "parallelism": "single-gpu",
+        },
+        "logprob_tokens_per_s": round(N / (l_ms * 1e-3), 1),
+        "roofline": dominant,
+        "rooflines": {"sampler": roof_s, "logprob": roof_l},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        cw = W.sampler_workload(5, device="cpu", rows=32)
+        clx, clt = W.logprob_workload(5, device="cpu", rows=64)
+        line["cpu_baseline"] = cpu_baseline(cw, clx, clt)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,212 @@
+// torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
+//
+// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, lse_partial,
+// lse_finalize}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// Python RuntimeError), allocates the outputs on the logits' device, and
+// enqueues the HIP kernels on the stream handle passed in from Python
+// (torch.cuda.current_stream().cuda_stream), so work orders with the
+// caller's other torch work exactly as the reference's ATen ops did.
+#include <ATen/ATen.h>
+#include <torch/library.h>
+
+#include <tuple>
+
+#include "graspo_tokpath.h"
+
+namespace {
+
+int dtype_code(const at::Tensor& t) {
+  switch (t.scalar_type()) {
+    case at::kFloat:
+      return GTP_DTYPE_F32;
+    case at::kBFloat16:
+      return GTP_DTYPE_BF16;
+    case at::kHalf:
+      return GTP_DTYPE_F16;
+    default:
+      TORCH_CHECK(false, "graspo_tokpath: logits must be float32, bfloat16 or float16, got ",
+                  t.scalar_type());
+  }
+  return -1;
+}
+
+void check_rc(int rc, const char* what) {
+  TORCH_CHECK(rc == GTP_OK, "graspo_tokpath: ", what, " failed with code ", rc,
+              rc == GTP_ERR_INVALID_ARGUMENT ? " (invalid argument)"
+              : rc == GTP_ERR_UNSUPPORTED    ? " (unsupported shape)"
+                                             : " (kernel launch error)");
+}
+
+void check_rows(const at::Tensor& logits, const char* name) {
+  TORCH_CHECK(logits.is_cuda(), "graspo_tokpath: ", name, " must be a GPU tensor");
+  TORCH_CHECK(logits.dim() == 2, "graspo_tokpath: ", name, " must be 2-D [rows, V], got ",
+              logits.dim(), "-D");
+  TORCH_CHECK(logits.size(1) == 0 || logits.stride(1) == 1, "graspo_tokpath: ", name,
+              " rows must be contiguous (stride(-1) == 1)");
+}
+
+int64_t row_stride_of(const at::Tensor& logits) {
+  return logits.size(0) > 1 ? logits.stride(0) : logits.size(1);
+}
+
+void check_same_device(const at::Tensor& a, const at::Tensor& b, const char* name) {
+  TORCH_CHECK(b.device() == a.device(), "graspo_tokpath: ", name, " must be on ", a.device());
+}
+
+using SampleOut =
+    std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor>;
+
+SampleOut sample(const at::Tensor& logits, double temperature, int64_t top_k, double top_p,
+                 double repetition_penalty, const c10::optional<at::Tensor>& history,
+                 const c10::optional<at::Tensor>& allow_mask,
+                 const c10::optional<at::Tensor>& uniforms,
+                 const c10::optional<at::Tensor>& finished, int64_t pad_token_id, int64_t stream) {
+  check_rows(logits, "logits");
+  const int64_t B = logits.size(0), V = logits.size(1);
+  TORCH_CHECK(V > 0, "graspo_tokpath.sample: empty vocabulary");
+  TORCH_CHECK(V <= GTP_SAMPLER_MAX_V, "graspo_tokpath.sample: V = ", V, " exceeds ",
+              GTP_SAMPLER_MAX_V);
+  TORCH_CHECK(repetition_penalty > 0.0, "graspo_tokpath.sample: repetition_penalty must be > 0");
+  TORCH_CHECK(top_k >= 0 && top_k <= INT32_MAX, "graspo_tokpath.sample: top_k must be >= 0");
+  const int32_t* hist = nullptr;
+  int64_t hist_len = 0, hist_stride = 0;
+  if (history.has_value() && history->numel() > 0) {
+    const auto& h = *history;
+    check_same_device(logits, h, "history");
+    TORCH_CHECK(h.scalar_type() == at::kInt && h.dim() == 2 && h.size(0) == B && h.stride(1) == 1,
+                "graspo_tokpath.sample: history must be int32 [B, L] with contiguous rows");
+    hist = h.data_ptr<int32_t>();
+    hist_len = h.size(1);
+    hist_stride = B > 1 ? h.stride(0) : hist_len;
+  }
+  const uint32_t* mask = nullptr;
+  int64_t mask_stride = 0;
+  if (allow_mask.has_value()) {
+    const auto& m = *allow_mask;
+    check_same_device(logits, m, "allow_mask");
+    TORCH_CHECK((m.scalar_type() == at::kInt || m.scalar_type() == at::kUInt32) && m.dim() == 2 &&
+                    m.size(0) == B && m.size(1) >= (V + 31) / 32 && m.stride(1) == 1,
+                "graspo_tokpath.sample: allow_mask must be int32/uint32 [B, >= ceil(V/32)]");
+    mask = static_cast<const uint32_t*>(m.data_ptr());
+    mask_stride = B > 1 ? m.stride(0) : m.size(1);
+  }
+  const bool greedy = !(temperature > 0.0);
+  const float* u = nullptr;
+  if (uniforms.has_value()) {
+    const auto& uu = *uniforms;
+    check_same_device(logits, uu, "uniforms");
+    TORCH_CHECK(uu.scalar_type() == at::kFloat && uu.dim() == 1 && uu.size(0) == B &&
+                    uu.is_contiguous(),
+                "graspo_tokpath.sample: uniforms must be float32 [B]");
+    u = uu.data_ptr<float>();
+  }
+  TORCH_CHECK(greedy || u != nullptr, "graspo_tokpath.sample: uniforms are required when T > 0");
+  const uint8_t* fin = nullptr;
+  if (finished.has_value()) {
+    const auto& f = *finished;
+    check_same_device(logits, f, "finished");
+    TORCH_CHECK((f.scalar_type() == at::kBool || f.scalar_type() == at::kByte) && f.dim() == 1 &&
+                    f.size(0) == B && f.is_contiguous(),
+                "graspo_tokpath.sample: finished must be bool/uint8 [B]");
+    fin = static_cast<const uint8_t*>(f.data_ptr());
+  }
+  auto opt = logits.options();
+  at::Tensor ids = at::empty({B}, opt.dtype(at::kLong));
+  at::Tensor lp = at::empty({B}, opt.dtype(at::kFloat));
+  at::Tensor slp = at::empty({B}, opt.dtype(at::kFloat));
+  at::Tensor kept = at::empty({B}, opt.dtype(at::kInt));
+  at::Tensor tv = at::empty({B}, opt.dtype(at::kFloat));
+  at::Tensor tid = at::empty({B}, opt.dtype(at::kInt));
+  at::Tensor st = at::empty({B}, opt.dtype(at::kInt));
+  gtp_sampler_params p;
+  p.temperature = (float)temperature;
+  p.top_k = (int32_t)top_k;
+  p.top_p = (float)top_p;
+  p.repetition_penalty = (float)repetition_penalty;
+  const int rc = gtp_sample_rows(
+      logits.data_ptr(), dtype_code(logits), B, V, row_stride_of(logits), hist, hist_len,
+      hist_stride, mask, mask_stride, u, &p, fin, pad_token_id, ids.data_ptr<int64_t>(),
+      lp.data_ptr<float>(), slp.data_ptr<float>(), kept.data_ptr<int32_t>(), tv.data_ptr<float>(),
+      tid.data_ptr<int32_t>(), st.data_ptr<int32_t>(), reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_sample_rows");
+  return {ids, lp, slp, kept, tv, tid, st};
+}
+
+const void* targets_ptr(const at::Tensor& logits, const at::Tensor& targets, int64_t N,
+                        int* is64) {
+  check_same_device(logits, targets, "targets");
+  TORCH_CHECK((targets.scalar_type() == at::kInt || targets.scalar_type() == at::kLong) &&
+                  targets.dim() == 1 && targets.size(0) == N && targets.is_contiguous(),
+              "graspo_tokpath: targets must be int32/int64 [N] contiguous");
+  *is64 = targets.scalar_type() == at::kLong;
+  return targets.data_ptr();
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> logprob_entropy(const at::Tensor& logits,
+                                                               const at::Tensor& targets,
+                                                               int64_t stream) {
+  check_rows(logits, "logits");
+  const int64_t N = logits.size(0), V = logits.size(1);
+  TORCH_CHECK(V > 0, "graspo_tokpath.logprob_entropy: empty vocabulary");
+  int t64 = 0;
+  const void* tp = targets_ptr(logits, targets, N, &t64);
+  auto opt = logits.options();
+  at::Tensor lp = at::empty({N}, opt.dtype(at::kFloat));
+  at::Tensor H = at::empty({N}, opt.dtype(at::kFloat));
+  at::Tensor st = at::empty({N}, opt.dtype(at::kInt));
+  const int rc = gtp_logprob_entropy_rows(logits.data_ptr(), dtype_code(logits), N, V,
+                                          row_stride_of(logits), tp, t64, lp.data_ptr<float>(),
+                                          H.data_ptr<float>(), st.data_ptr<int32_t>(),
+                                          reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_logprob_entropy_rows");
+  return {lp, H, st};
+}
+
+void lse_partial(const at::Tensor& logits, const c10::optional<at::Tensor>& targets,
+                 int64_t col_offset, const at::Tensor& state, bool accumulate, int64_t stream) {
+  check_rows(logits, "logits");
+  const int64_t N = logits.size(0), Vc = logits.size(1);
+  TORCH_CHECK(Vc > 0, "graspo_tokpath.lse_partial: empty chunk");
+  check_same_device(logits, state, "state");
+  TORCH_CHECK(state.scalar_type() == at::kFloat && state.dim() == 2 && state.size(0) == N &&
+                  state.size(1) == 4 && state.is_contiguous(),
+              "graspo_tokpath.lse_partial: state must be float32 [N, 4] contiguous");
+  int t64 = 0;
+  const void* tp = nullptr;
+  if (targets.has_value()) tp = targets_ptr(logits, *targets, N, &t64);
+  const int rc = gtp_lse_partial_rows(logits.data_ptr(), dtype_code(logits), N, Vc,
+                                      row_stride_of(logits), col_offset, tp, t64,
+                                      state.data_ptr<float>(), accumulate ? 1 : 0,
+                                      reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_lse_partial_rows");
+}
+
+std::tuple<at::Tensor, at::Tensor> lse_finalize(const at::Tensor& state, int64_t stream) {
+  TORCH_CHECK(state.is_cuda() && state.scalar_type() == at::kFloat && state.dim() == 2 &&
+                  state.size(1) == 4 && state.is_contiguous(),
+              "graspo_tokpath.lse_finalize: state must be a float32 [N, 4] GPU tensor");
+  const int64_t N = state.size(0);
+  at::Tensor lp = at::empty({N}, state.options());
+  at::Tensor H = at::empty({N}, state.options());
+  const int rc = gtp_lse_finalize_rows(state.data_ptr<float>(), N, lp.data_ptr<float>(),
+                                       H.data_ptr<float>(), reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_lse_finalize_rows");
+  return {lp, H};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(graspo_tokpath, m) {
+  m.def(
+      "sample(Tensor logits, float temperature, int top_k, float top_p, float repetition_penalty, "
+      "Tensor? history, Tensor? allow_mask, Tensor? uniforms, Tensor? finished, int pad_token_id, "
+      "int stream) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)",
+      &sample);
+  m.def("logprob_entropy(Tensor logits, Tensor targets, int stream) -> (Tensor, Tensor, Tensor)",
+        &logprob_entropy);
+  m.def(
+      "lse_partial(Tensor logits, Tensor? targets, int col_offset, Tensor(a!) state, "
+      "bool accumulate, int stream) -> ()",
+      &lse_partial);
+  m.def("lse_finalize(Tensor state, int stream) -> (Tensor, Tensor)", &lse_finalize);
+}

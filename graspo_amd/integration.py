@@ -1,0 +1,80 @@
+"""Install the gfx950 drop-ins into an imported ``graspo`` package.
+
+The reference's adapters import the hot-path helpers *by name* at module
+level (e.g. ``src/graspo/backends/graspoflow/models/qwen35_36/generation.py:20-24``,
+``models/qwen3/adapter.py:25-32``), and Python resolves such names through
+each importing module's globals at call time.  Rebinding those globals is
+therefore enough: no reference call site is edited.
+
+    import graspo_amd.integration as gi
+    patched = gi.install()      # after graspo is importable
+    ...
+    gi.uninstall()
+"""
+
+from __future__ import annotations
+
+import importlib
+
+from . import graspo_loss as _loss
+from . import tensor_utils as _tu
+
+_TU = "graspo.backends.graspoflow.tensor_utils"
+_SAMPLER_NAMES = ("_next_token_from_logits", "_sample_next_token", "_broadcast_and_pad_finished")
+_LOGPROB_NAMES = ("_selected_token_log_probs_from_hidden",)
+
+# module -> names it binds (from the reference's import lists)
+TARGETS: dict[str, tuple[str, ...]] = {
+    _TU: _SAMPLER_NAMES + _LOGPROB_NAMES,
+    "graspo.backends.graspoflow.models.qwen35_36.generation": _SAMPLER_NAMES,
+    "graspo.backends.graspoflow.models.qwen3.adapter": _SAMPLER_NAMES,
+    "graspo.backends.graspoflow.models.qwen3.model": _LOGPROB_NAMES,
+    "graspo.backends.graspoflow.models.qwen35_36.model": _LOGPROB_NAMES,
+    "graspo.backends.graspoflow.models.qwen35_36.logprobs": _LOGPROB_NAMES,
+    "graspo.backends.graspoflow.models.qwen35_36.training": _LOGPROB_NAMES,
+    "graspo.backends.graspoflow.transformer_adapter": _LOGPROB_NAMES,
+    "graspo.core.graspo_loss": ("sequence_log_probs_from_logits",),
+}
+
+REPLACEMENTS = {
+    "_next_token_from_logits": _tu._next_token_from_logits,
+    "_sample_next_token": _tu._sample_next_token,
+    "_broadcast_and_pad_finished": _tu._broadcast_and_pad_finished,
+    "_selected_token_log_probs_from_hidden": _tu._selected_token_log_probs_from_hidden,
+    "sequence_log_probs_from_logits": _loss.sequence_log_probs_from_logits,
+}
+
+_saved: dict[tuple[str, str], object] = {}
+
+
+def install(targets: dict[str, tuple[str, ...]] | None = None, *, strict: bool = False):
+    """Rebind the hot-path names in every importable target module.
+
+    Returns the list of ``(module, name)`` pairs that were replaced.  With
+    ``strict`` a module that cannot be imported raises; otherwise it is
+    skipped (a model family that is not installed)."""
+    done = []
+    for mod_name, names in (targets or TARGETS).items():
+        try:
+            mod = importlib.import_module(mod_name)
+        except ImportError:
+            if strict:
+                raise
+            continue
+        for name in names:
+            if not hasattr(mod, name):
+                continue
+            key = (mod_name, name)
+            if key not in _saved:
+                _saved[key] = getattr(mod, name)
+            setattr(mod, name, REPLACEMENTS[name])
+            done.append(key)
+    return done
+
+
+def uninstall() -> None:
+    """Restore every name :func:`install` replaced."""
+    for (mod_name, name), orig in list(_saved.items()):
+        mod = importlib.import_module(mod_name)
+        setattr(mod, name, orig)
+        del _saved[(mod_name, name)]

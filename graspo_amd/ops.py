@@ -1,0 +1,131 @@
+"""Tensor-level entry points of the gfx950 token path.
+
+Each function validates nothing beyond what the native op checks, enqueues
+the HIP kernels on the caller's current stream and returns device tensors;
+none of them synchronises the host.
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import load
+
+ROW_OK, ROW_NONFINITE, ROW_EMPTY, ROW_BAD_HISTORY, ROW_BAD_UNIFORM, ROW_BAD_TARGET = range(6)
+STATUS_NAMES = {
+    ROW_OK: "ok",
+    ROW_NONFINITE: "non-finite logits",
+    ROW_EMPTY: "no allowed token",
+    ROW_BAD_HISTORY: "history id >= V",
+    ROW_BAD_UNIFORM: "uniform outside [0, 1)",
+    ROW_BAD_TARGET: "target outside [0, V)",
+}
+
+
+class SampleOutput(NamedTuple):
+    ids: torch.Tensor              # int64 [B]
+    logprob: torch.Tensor          # fp32 [B], log_softmax(raw row)[id]
+    sampled_logprob: torch.Tensor  # fp32 [B], log of the final sampling probability
+    kept: torch.Tensor             # int32 [B], size of the kept (top-k/top-p) set
+    thresh_value: torch.Tensor     # fp32 [B], processed logit of the last kept rank
+    thresh_id: torch.Tensor        # int32 [B], id of the last kept rank
+    status: torch.Tensor           # int32 [B], 0 = ok
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _as_rows(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if logits.dim() != 2:
+        raise ValueError(f"expected [rows, V] logits, got shape {tuple(logits.shape)}")
+    if logits.size(1) > 0 and logits.stride(1) != 1:
+        logits = logits.contiguous()
+    return logits
+
+
+def draw_uniforms(batch: int, device, generator: torch.Generator | None = None) -> torch.Tensor:
+    """U(0,1) draws on the 2^-24 grid from torch's generator (the same RNG
+    stream the reference's torch.multinomial consumes, so a restored RNG state
+    reproduces the draws)."""
+    k = torch.randint(0, 1 << 24, (batch,), device=device, generator=generator, dtype=torch.int32)
+    return k.to(torch.float32) * (2.0 ** -24)
+
+
+def sample(
+    logits: torch.Tensor,
+    *,
+    temperature: float,
+    top_k: int = 0,
+    top_p: float = 1.0,
+    repetition_penalty: float = 1.0,
+    history: torch.Tensor | None = None,
+    allow_mask: torch.Tensor | None = None,
+    uniforms: torch.Tensor | None = None,
+    finished: torch.Tensor | None = None,
+    pad_token_id: int = 0,
+    generator: torch.Generator | None = None,
+) -> SampleOutput:
+    """One token per row of ``logits`` [B, V] (bf16 / fp16 / fp32; rows may be
+    strided, e.g. ``logits[:, -1, :]``).  See include/graspo_tokpath.h for the
+    exact contract.  ``uniforms`` default to draws from torch's generator."""
+    ops = load()
+    logits = _as_rows(logits)
+    B = logits.size(0)
+    if temperature > 0 and uniforms is None:
+        uniforms = draw_uniforms(B, logits.device, generator)
+    if history is not None and history.dtype != torch.int32:
+        history = history.to(torch.int32)
+    if finished is not None and finished.dtype not in (torch.bool, torch.uint8):
+        finished = finished.to(torch.bool)
+    out = ops.sample(
+        logits, float(temperature), int(top_k), float(top_p), float(repetition_penalty),
+        history, allow_mask, uniforms, finished, int(pad_token_id), _stream(logits),
+    )
+    return SampleOutput(*out)
+
+
+def logprob_entropy(logits: torch.Tensor, targets: torch.Tensor):
+    """(logprob, entropy, status) per row of ``logits`` [N, V]; one HBM read."""
+    ops = load()
+    logits = _as_rows(logits)
+    targets = targets.reshape(-1)
+    if targets.dtype not in (torch.int32, torch.int64):
+        targets = targets.to(torch.int64)
+    return ops.logprob_entropy(logits, targets.contiguous(), _stream(logits))
+
+
+def lse_partial(logits_chunk: torch.Tensor, targets: torch.Tensor | None, col_offset: int,
+                state: torch.Tensor, accumulate: bool) -> None:
+    """Fold a vocabulary chunk into the running (m, s, t, x_target) row state."""
+    ops = load()
+    logits_chunk = _as_rows(logits_chunk)
+    if targets is not None:
+        targets = targets.reshape(-1).contiguous()
+    ops.lse_partial(logits_chunk, targets, int(col_offset), state, bool(accumulate),
+                    _stream(logits_chunk))
+
+
+def lse_finalize(state: torch.Tensor):
+    """(logprob, entropy) from a chunk state."""
+    ops = load()
+    return ops.lse_finalize(state, _stream(state))
+
+
+def new_lse_state(rows: int, device) -> torch.Tensor:
+    return torch.empty((rows, 4), dtype=torch.float32, device=device)
+
+
+def raise_on_bad_status(status: torch.Tensor, what: str) -> None:
+    """Host check (one device sync) mirroring the reference's errors on
+    invalid rows (torch.multinomial rejects NaN/inf probabilities)."""
+    bad = status.ne(ROW_OK)
+    if bool(bad.any()):
+        codes = sorted({int(c) for c in status[bad].tolist()})
+        rows = bad.nonzero().flatten()[:8].tolist()
+        names = ", ".join(STATUS_NAMES.get(c, str(c)) for c in codes)
+        raise RuntimeError(f"{what}: invalid rows {rows} ({names})")

@@ -1,0 +1,175 @@
+/*
+ * graspo_tokpath.h -- C ABI of the MI355X (gfx950) vocabulary-wide token path.
+ *
+ * Two operations, both HBM-bound streaming passes over [rows, V] logits:
+ *
+ *   1. gtp_sample_rows: the rollout sampler.  Per row: repetition penalty,
+ *      allow-mask, temperature, top-k, top-p and an inverse-CDF draw from a
+ *      caller-supplied uniform.  Bit-exact and deterministic: the draw uses
+ *      fixed-point weights (see "Sampler contract" below), so the same inputs
+ *      give the same ids on any device, in any reduction order.
+ *   2. gtp_logprob_entropy_rows / gtp_lse_partial_rows: the per-token
+ *      selective log-softmax gather and the softmax entropy, fp32 accumulation.
+ *
+ * Conventions shared by every entry point:
+ *   - All array pointers are DEVICE pointers owned by the caller.  The library
+ *     never allocates, keeps no mutable global state and is reentrant.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
+ *     void*; NULL is the default stream).
+ *   - Return value: GTP_OK or a GTP_ERR_* code for a bad argument or a failed
+ *     launch.  Data-dependent problems of a single row are reported per row
+ *     through `out_status` (GTP_ROW_*), never through the return value.
+ *   - Logits rows are `row_stride` elements apart (row_stride >= V), so a
+ *     [B, S, V] tensor's last position can be passed without a copy.
+ *
+ * Sampler contract (per row; every step is one IEEE-754 fp32 operation):
+ *   x_i   = float(logits[i])                         (bf16/fp16 -> fp32 is exact)
+ *   status NONFINITE if any x_i is NaN or +inf; BAD_HISTORY if any history
+ *   id >= V (ids < 0 are padding); BAD_UNIFORM unless 0 <= u < 1.
+ *   x'_i  = i in set(history) ? (x_i < 0 ? x_i * rho : x_i / rho) : x_i
+ *   allowed_i = mask == NULL || bit (i & 31) of mask[i >> 5] is set
+ *   y_i   = T > 0 ? x'_i / max(T, 1e-6f) : x'_i
+ *   valid = { i : allowed_i and y_i > -inf };  empty -> status EMPTY
+ *   order = (y desc, id asc); NONFINITE if the largest y is +inf
+ *   T <= 0 (greedy): id = first in order; kept = 1; sampled_logprob = 0.
+ *   top-k: if 0 < K < |valid| keep the first K, else keep all valid.
+ *   m = y of the first in order; w_i = DETEXP_FIX(y_i - m) (uint64, 2^40 = 1.0)
+ *   top-p: if 0 < P < 1, with W = sum of kept w and S_r = sum_{j<r} w_j,
+ *          keep rank r iff S_r <= floor(P * W)  (first rank always kept).
+ *   draw:  W' = sum of kept w; U = floor(u * W'); id = first rank r with
+ *          S_{r+1} > U.
+ *   outputs: id; kept = |kept set|; threshold (y, id) of the last kept rank;
+ *            logprob = log_softmax(x)[id] (unpenalized, unmasked, T = 1);
+ *            sampled_logprob = log(w_id / W').
+ *   A row with status != OK gets id = -1, kept = 0, NaN logprobs.
+ *
+ * DETEXP_FIX(d) for d <= 0 (all fp32 except the last step):
+ *   d < -30 -> 0;  n = rint(d * 0x1.715476p+0);
+ *   r = fma(-n, 0x1.62e4p-1, d);  r = fma(-n, 0x1.7f7d1cp-20, r);
+ *   p = Horner(r; 1/7! .. 1/2!, 1, 1) with fma, coefficients rounded to fp32;
+ *   result = p * 2^(n + 40) rounded to an integer, ties to even.
+ */
+#ifndef GRASPO_TOKPATH_H
+#define GRASPO_TOKPATH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of the logits. */
+enum gtp_dtype {
+  GTP_DTYPE_F32 = 0,
+  GTP_DTYPE_BF16 = 1,
+  GTP_DTYPE_F16 = 2
+};
+
+/* Return codes. */
+enum gtp_error {
+  GTP_OK = 0,
+  GTP_ERR_INVALID_ARGUMENT = 1,
+  GTP_ERR_UNSUPPORTED = 2,
+  GTP_ERR_LAUNCH = 3
+};
+
+/* Per-row status codes written to out_status. */
+enum gtp_row_status {
+  GTP_ROW_OK = 0,
+  GTP_ROW_NONFINITE = 1,   /* NaN or +inf in the row (or +inf after temperature) */
+  GTP_ROW_EMPTY = 2,       /* no allowed token with a finite processed logit */
+  GTP_ROW_BAD_HISTORY = 3, /* a history id >= V */
+  GTP_ROW_BAD_UNIFORM = 4, /* uniform outside [0, 1) */
+  GTP_ROW_BAD_TARGET = 5   /* logprob target outside [0, V) */
+};
+
+/* Largest vocabulary the sampler handles (the per-row penalty bitmap and
+ * candidate index live in LDS). */
+#define GTP_SAMPLER_MAX_V (1 << 18)
+
+typedef struct gtp_sampler_params {
+  float temperature;        /* <= 0 selects greedy decoding */
+  int32_t top_k;            /* 0 (or >= number of valid tokens) disables top-k */
+  float top_p;              /* active iff 0 < top_p < 1 */
+  float repetition_penalty; /* 1 disables; must be > 0 */
+} gtp_sampler_params;
+
+/*
+ * gtp_sample_rows -- one sampled token per row.
+ *
+ * Replaces the reference's per-step sampler
+ *   _next_token_from_logits  src/graspo/backends/graspoflow/tensor_utils.py:649-658
+ *   _sample_next_token       src/graspo/backends/graspoflow/tensor_utils.py:671-683
+ * (temperature, greedy argmax, softmax / sort / cumsum / top-p cut /
+ * multinomial) and extends it with repetition penalty, allow-mask, top-k and
+ * a supplied-uniform draw.
+ *
+ *   logits      [B, row_stride] of `dtype`, first V entries of each row used
+ *   history     [B, hist_stride] int32, first hist_len used (NULL or
+ *               hist_len == 0: no penalty)
+ *   allow_mask  [B, mask_stride] uint32, mask_stride >= ceil(V/32), LSB-first
+ *               (NULL: every token allowed)
+ *   uniforms    [B] fp32 in [0, 1) (ignored for greedy rows; may be NULL then)
+ *   finished    [B] uint8 or NULL; rows with finished[b] != 0 output
+ *               pad_token_id as their id (the where() of
+ *               _broadcast_and_pad_finished, tensor_utils.py:661-668)
+ *   outputs     [B] each; any of them may be NULL except out_ids.
+ */
+int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
+                    int64_t row_stride, const int32_t* history, int64_t hist_len,
+                    int64_t hist_stride, const uint32_t* allow_mask,
+                    int64_t mask_stride, const float* uniforms,
+                    const gtp_sampler_params* params, const uint8_t* finished,
+                    int64_t pad_token_id, int64_t* out_ids, float* out_logprob,
+                    float* out_sampled_logprob, int32_t* out_kept,
+                    float* out_thresh_value, int32_t* out_thresh_id,
+                    int32_t* out_status, void* stream);
+
+/*
+ * gtp_logprob_entropy_rows -- log_softmax(x)[target] and softmax entropy per
+ * row, one streaming read of the row, fp32 accumulation.
+ *
+ * Replaces sequence_log_probs_from_logits  src/graspo/core/graspo_loss.py:19-21
+ * (log_softmax over V, gather) without writing the [N, V] log-softmax; the
+ * entropy -sum p log p has no reference counterpart.
+ *
+ *   targets      [N] int32 (targets_int64 == 0) or int64 token ids
+ *   out_logprob  [N] fp32; out_entropy [N] fp32 or NULL; out_status [N] or NULL
+ * A target outside [0, V) gives NaN logprob and GTP_ROW_BAD_TARGET.
+ */
+int gtp_logprob_entropy_rows(const void* logits, int dtype, int64_t N,
+                             int64_t V, int64_t row_stride, const void* targets,
+                             int targets_int64, float* out_logprob,
+                             float* out_entropy, int32_t* out_status,
+                             void* stream);
+
+/*
+ * gtp_lse_partial_rows -- fold one vocabulary chunk [col_offset, col_offset+Vc)
+ * into a running per-row state (m, s, t, x_target), all fp32:
+ *   m = running max, s = sum exp(x - m), t = sum exp(x - m) * (x - m),
+ *   x_target = the target's logit once its chunk has been seen (else NaN).
+ * accumulate == 0 starts a new state; != 0 merges into `state`.
+ *
+ * Replaces the vocabulary-chunk loop of _selected_token_log_probs_from_hidden
+ * src/graspo/backends/graspoflow/tensor_utils.py:180-186 (logsumexp per chunk,
+ * logaddexp across chunks); the chunk logits come from the caller's GEMM.
+ */
+int gtp_lse_partial_rows(const void* logits, int dtype, int64_t N, int64_t Vc,
+                         int64_t row_stride, int64_t col_offset,
+                         const void* targets, int targets_int64, float* state,
+                         int accumulate, void* stream);
+
+/* gtp_lse_finalize_rows -- logprob = x_target - m - log s and
+ * entropy = log s - t / s from the state of gtp_lse_partial_rows. */
+int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_logprob,
+                          float* out_entropy, void* stream);
+
+/* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
+const char* gtp_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRASPO_TOKPATH_H */

@@ -1,0 +1,174 @@
+"""GPU parity of the sampler kernel against the exact CPU oracle.
+
+Ids, kept-set sizes, thresholds and statuses must be bit-exact; the two
+logprob outputs within 1e-3 absolute.  Covers the four sampler workloads at
+full size and the edge cases of the contract (statuses, ties, greedy,
+dtypes, strided rows, odd V, the general path)."""
+
+import numpy as np
+import pytest
+import torch
+
+from graspo_amd import ops
+from graspo_amd import workloads as W
+from oracle import oracle as O
+from tests._util import oracle_sample
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _to(t, dev):
+    return None if t is None else t.to(dev)
+
+
+def gpu_sample(logits, **kw):
+    dev = torch.device("cuda:0")
+    kw = {k: (_to(v, dev) if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    out = ops.sample(logits.to(dev), **kw)
+    torch.cuda.synchronize()
+    return ops.SampleOutput(*[t.cpu() for t in out])
+
+
+def assert_parity(g, ref, what=""):
+    st = g.status.numpy()
+    assert np.array_equal(st, ref.status), (what, st, ref.status)
+    assert np.array_equal(g.ids.numpy(), ref.ids), (what, g.ids.numpy(), ref.ids)
+    ok = ref.status == 0
+    assert np.array_equal(g.kept.numpy()[ok], ref.kept[ok]), what
+    assert np.array_equal(g.thresh_id.numpy()[ok], ref.thresh_id[ok]), what
+    assert np.array_equal(g.thresh_value.numpy()[ok].view(np.uint32),
+                          ref.thresh_value[ok].view(np.uint32)), what
+    if ok.any():
+        assert np.abs(g.logprob.numpy()[ok] - ref.logprob[ok]).max() <= TOL, what
+        assert np.abs(g.sampled_logprob.numpy()[ok] - ref.sampled_logprob[ok]).max() <= TOL, what
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 5])
+def test_workload_parity(cfg):
+    wl = W.sampler_workload(cfg)
+    print(f"workload {cfg} shape {wl.shape}", flush=True)
+    ref = oracle_sample(wl.logits, **wl.kwargs())
+    g = gpu_sample(wl.logits, **wl.kwargs())
+    assert_parity(g, ref, f"cfg{cfg}")
+    for r, t in wl.single_rows.items():
+        assert int(g.ids[r]) == t
+
+
+@pytest.mark.parametrize("cfg", [1, 5])
+@pytest.mark.parametrize("variant", ["greedy", "top_p_only", "top_k_300", "rho_below_1"])
+def test_workload_variants(cfg, variant):
+    """The same inputs through the other selection paths (greedy, general
+    path for top-p only / large k / rho < 1)."""
+    wl = W.sampler_workload(cfg, rows=16)
+    kw = wl.kwargs()
+    if variant == "greedy":
+        kw["temperature"] = 0.0
+    elif variant == "top_p_only":
+        kw["top_k"] = 0
+    elif variant == "top_k_300":
+        kw["top_k"] = 300
+    else:
+        kw["repetition_penalty"] = 0.8
+    print(f"cfg {cfg} variant {variant}", flush=True)
+    assert_parity(gpu_sample(wl.logits, **kw), oracle_sample(wl.logits, **kw), variant)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [1000, 1001, 4099, 32768 + 5])
+def test_dtypes_and_odd_vocab(dtype, V):
+    g = torch.Generator().manual_seed(V)
+    x = (torch.randn(6, V, generator=g) * 3).to(dtype)
+    u = W.uniforms_24(6, g, "cpu")
+    hist = torch.randint(0, V, (6, 17), generator=g, dtype=torch.int32)
+    for kw in (dict(temperature=0.7, top_k=20, top_p=0.9, repetition_penalty=1.1, history=hist),
+               dict(temperature=1.3, top_k=0, top_p=0.8),
+               dict(temperature=0.0)):
+        print(dtype, V, kw.keys(), flush=True)
+        assert_parity(gpu_sample(x, uniforms=u, **kw), oracle_sample(x, uniforms=u, **kw))
+
+
+def test_strided_rows_last_position():
+    """logits[:, -1, :] of a [B, S, V] tensor (the call-site layout)."""
+    g = torch.Generator().manual_seed(1)
+    full = (torch.randn(5, 3, 2000, generator=g) * 2).to(torch.bfloat16)
+    u = W.uniforms_24(5, g, "cpu")
+    dev = torch.device("cuda:0")
+    view = full.to(dev)[:, -1, :]
+    assert view.stride(0) == 3 * 2000
+    out = ops.sample(view, temperature=0.9, top_k=10, uniforms=u.to(dev))
+    ref = oracle_sample(full[:, -1, :].contiguous(), temperature=0.9, top_k=10, uniforms=u)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.ids.cpu().numpy(), ref.ids)
+
+
+def test_status_rows_and_padding():
+    V = 300
+    x = torch.zeros(8, V)
+    x[0, 3] = float("nan")
+    x[1, 4] = float("inf")
+    bits = torch.ones(8, V, dtype=torch.bool)
+    bits[2] = False
+    bits[3] = False
+    bits[3, 39] = True
+    hist = torch.full((8, 2), -1, dtype=torch.int32)
+    hist[4, 1] = V
+    u = torch.full((8,), 0.5)
+    u[5] = 1.0
+    x[6] = float("-inf")
+    x[7] = torch.arange(V, dtype=torch.float32) % 7
+    fin = torch.zeros(8, dtype=torch.bool)
+    fin[7] = True
+    kw = dict(temperature=1.0, repetition_penalty=1.2, history=hist,
+              allow_mask=W.pack_mask(bits), uniforms=u, finished=fin, pad_token_id=-5)
+    assert_parity(gpu_sample(x, **kw), oracle_sample(x, **kw))
+
+
+@pytest.mark.parametrize("top_k", [0, 1, 7, 256, 257, 5000])
+def test_heavy_ties(top_k):
+    """Uniform and few-valued rows: ties resolve by id (radix fallback when
+    the tied bin overflows the collector)."""
+    V = 20000
+    x = torch.zeros(4, V, dtype=torch.bfloat16)
+    x[1] = (torch.arange(V) % 3).to(torch.bfloat16)
+    x[2, 100:200] = 5.0
+    x[3] = (torch.arange(V) % 50).to(torch.bfloat16) * 0.25
+    u = torch.tensor([0.0, 0.37, 0.999, 1 - 2**-24])
+    for p in (1.0, 0.6):
+        kw = dict(temperature=0.5, top_k=top_k, top_p=p, uniforms=u)
+        print("ties", top_k, p, flush=True)
+        assert_parity(gpu_sample(x, **kw), oracle_sample(x, **kw), f"k{top_k} p{p}")
+
+
+def test_uniform_edges_and_single_allowed():
+    g = torch.Generator().manual_seed(9)
+    V = 151936
+    x = (torch.randn(6, V, generator=g) * 2.5).to(torch.bfloat16)
+    bits = torch.rand(6, V, generator=g) < 0.001
+    bits[4] = False
+    bits[4, 77777] = True
+    bits[5] = False
+    bits[5, V - 1] = True
+    u = torch.tensor([0.0, 2**-24, 0.5, 1 - 2**-24, 0.25, 0.75])
+    kw = dict(temperature=0.8, top_p=0.9, allow_mask=W.pack_mask(bits), uniforms=u)
+    g_out = gpu_sample(x, **kw)
+    assert_parity(g_out, oracle_sample(x, **kw))
+    assert int(g_out.ids[4]) == 77777 and int(g_out.ids[5]) == V - 1
+
+
+def test_deterministic_repeat():
+    wl = W.sampler_workload(5, rows=32)
+    a = gpu_sample(wl.logits, **wl.kwargs())
+    b = gpu_sample(wl.logits, **wl.kwargs())
+    assert torch.equal(a.ids, b.ids) and torch.equal(a.sampled_logprob, b.sampled_logprob)
+
+
+def test_rejects_cpu_tensors_and_bad_args():
+    x = torch.zeros(2, 10)
+    with pytest.raises(RuntimeError):
+        ops.sample(x, temperature=0.0)
+    xd = x.cuda()
+    with pytest.raises(RuntimeError):
+        ops.sample(xd, temperature=1.0, repetition_penalty=0.0, uniforms=torch.zeros(2).cuda())
+    with pytest.raises(RuntimeError):
+        ops.sample(torch.zeros(2, (1 << 18) + 8).cuda(), temperature=0.0)

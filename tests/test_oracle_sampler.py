@@ -1,0 +1,202 @@
+"""Pins of the exact sampler oracle (oracle/tokpath_oracle.c).
+
+Each check is independent of the oracle's own arithmetic: the fp64 literal
+restatement of the reference sampler (tensor_utils.py:649-683), exhaustive
+uniform grids against exact fp64 softmax probabilities on tiny rows,
+transformers' RepetitionPenaltyLogitsProcessor, torch.topk / torch.argmax,
+and closed forms (uniform rows, single allowed token, status rows).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from graspo_amd import workloads as W
+from oracle import oracle as O
+from tests._util import logits_to_oracle, oracle_sample
+
+
+def _sem(wl: W.SamplerWorkload):
+    a, dt = logits_to_oracle(wl.logits)
+    return O.sample_semantic(
+        O.bits_to_f32(a, dt), temperature=wl.temperature, top_k=wl.top_k, top_p=wl.top_p,
+        repetition_penalty=wl.repetition_penalty,
+        history=None if wl.history is None else wl.history.numpy(),
+        allow_mask=None if wl.allow_mask is None else wl.allow_mask.numpy(),
+        uniforms=wl.uniforms.numpy(),
+    )
+
+
+@pytest.mark.parametrize("cfg,rows", [(1, 8), (2, 12), (3, 16), (5, 16)])
+def test_exact_oracle_matches_semantic_restatement(cfg, rows):
+    wl = W.sampler_workload(cfg, rows=rows)
+    ex = oracle_sample(wl.logits, **wl.kwargs())
+    sem = _sem(wl)
+    assert (ex.status == O.ROW_OK).all()
+    for b, (sid, skept, cut_margin, draw_margin) in enumerate(sem):
+        if ex.ids[b] != sid or ex.kept[b] != skept:
+            # only a measured near-tie may separate fixed point from fp64
+            assert min(cut_margin, draw_margin) < 1e-9, (b, ex.ids[b], sid, ex.kept[b], skept)
+    for r, t in wl.single_rows.items():
+        assert ex.ids[r] == t and ex.kept[r] == 1
+
+
+def _exact_probs(y: np.ndarray, top_k: int, top_p: float):
+    """fp64 probabilities of the kept set of one row, in (y desc, id asc) order."""
+    order = sorted(range(len(y)), key=lambda i: (-y[i], i))
+    order = [i for i in order if y[i] > -np.inf]
+    if 0 < top_k < len(order):
+        order = order[:top_k]
+    e = np.array([math.exp(float(y[i]) - float(y[order[0]])) for i in order])
+    p = e / e.sum()
+    if 0 < top_p < 1:
+        excl = np.concatenate([[0.0], np.cumsum(p)[:-1]])
+        R = int((excl <= top_p).sum())
+        order, p = order[:R], p[:R] / p[:R].sum()
+    return order, p
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_tiny_rows_exhaustive_uniform_grid(seed):
+    """Every u on a 2^-12 grid: the frequency of each token equals its exact
+    probability within the grid resolution, and ids walk the order."""
+    rng = np.random.default_rng(seed)
+    V = int(rng.integers(3, 9))
+    x = (rng.standard_normal(V) * 2).astype(np.float32)[None, :]
+    T, K, P = 0.8, int(rng.integers(0, V + 1)), float(rng.choice([1.0, 0.7, 0.9]))
+    n = 4096
+    u = (np.arange(n, dtype=np.float64) / n).astype(np.float32)
+    X = np.repeat(x, n, axis=0)
+    r = O.sample_rows(X, O.DTYPE_F32, temperature=T, top_k=K, top_p=P, uniforms=u)
+    y = (x[0] / np.float32(T)).astype(np.float32)
+    order, p = _exact_probs(y, K, P)
+    assert set(r.kept.tolist()) == {len(order)}
+    freq = np.array([(r.ids == i).sum() / n for i in order])
+    assert np.abs(freq - p).max() <= 1.0 / n + 1e-6
+    assert set(r.ids.tolist()) <= set(order)
+    # monotone in u: ranks never go back
+    rank = {t: k for k, t in enumerate(order)}
+    ranks = [rank[i] for i in r.ids]
+    assert ranks == sorted(ranks)
+
+
+def test_uniform_row_closed_form():
+    """All logits equal: ties resolve by id, weights are equal, so the draw
+    is token floor(u * V) exactly."""
+    V = 1000
+    u = np.array([0.0, 0.5, 2.0**-24, 1 - 2.0**-24, 0.123456789], np.float32)
+    X = np.zeros((len(u), V), np.float32)
+    r = O.sample_rows(X, O.DTYPE_F32, temperature=1.0, uniforms=u)
+    want = np.floor(u.astype(np.float64) * V).astype(np.int64)
+    assert (r.ids == want).all()
+    assert (r.kept == V).all()
+
+
+def test_greedy_and_top1_are_argmax_first_index():
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((16, 777)).astype(np.float32)
+    X[3, [5, 9]] = 50.0  # tie: lowest id wins
+    g = O.sample_rows(X, O.DTYPE_F32, temperature=0.0)
+    k1 = O.sample_rows(X, O.DTYPE_F32, temperature=0.7, top_k=1,
+                       uniforms=rng.random(16).astype(np.float32))
+    want = torch.argmax(torch.from_numpy(X), dim=-1).numpy()
+    assert (g.ids == want).all() and (k1.ids == want).all()
+    assert g.ids[3] == 5 and (k1.kept == 1).all()
+    assert np.allclose(k1.sampled_logprob, 0.0)
+
+
+def test_top_k_set_matches_torch_topk():
+    rng = np.random.default_rng(4)
+    X = (rng.standard_normal((8, 5000)) * 3).astype(np.float32)  # no exact ties
+    K = 37
+    r = O.sample_rows(X, O.DTYPE_F32, temperature=0.9, top_k=K,
+                      uniforms=rng.random(8).astype(np.float32))
+    assert (r.kept == K).all()
+    top = torch.topk(torch.from_numpy(X), K, dim=-1)
+    for b in range(8):
+        assert r.ids[b] in set(top.indices[b].tolist())
+        # threshold = the K-th value / T, id of the K-th
+        assert r.thresh_id[b] == int(top.indices[b, -1])
+        assert r.thresh_value[b] == np.float32(top.values[b, -1].item()) / np.float32(0.9)
+
+
+def test_penalty_matches_hf_repetition_penalty():
+    from transformers.generation.logits_process import RepetitionPenaltyLogitsProcessor
+
+    rng = np.random.default_rng(5)
+    B, V, L = 12, 3000, 40
+    X = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    hist = rng.integers(0, V, (B, L)).astype(np.int32)
+    # make the row maximum a penalised token in most rows, positive or negative
+    for b in range(B):
+        hist[b, 0] = int(np.argmax(X[b]))
+        if b % 3 == 0:
+            X[b] -= 20.0
+    for rho in (1.05, 1.3, 0.9):
+        hf = RepetitionPenaltyLogitsProcessor(penalty=rho)(
+            torch.from_numpy(hist.astype(np.int64)), torch.from_numpy(X.copy())).numpy()
+        r = O.sample_rows(X, O.DTYPE_F32, temperature=1.0, top_k=1, repetition_penalty=rho,
+                          history=hist, uniforms=np.zeros(B, np.float32))
+        assert (r.ids == hf.argmax(-1)).all()
+        assert np.array_equal(r.thresh_value, hf.max(-1).astype(np.float32))
+        assert np.array_equal(O.penalize_f32(X, hist, rho), hf)
+
+
+def test_top_p_cut_invariant():
+    """Mass strictly before the last kept rank <= P; with one more rank it
+    would exceed P (fp64, away from near-ties)."""
+    wl = W.sampler_workload(2, rows=6)
+    ex = oracle_sample(wl.logits, **wl.kwargs())
+    a, dt = logits_to_oracle(wl.logits)
+    x = O.penalize_f32(O.bits_to_f32(a, dt), wl.history.numpy(), wl.repetition_penalty)
+    for b in range(6):
+        y = np.sort(x[b].astype(np.float64) / wl.temperature)[::-1]
+        p = np.exp(y - y[0])
+        p /= p.sum()
+        excl = np.concatenate([[0.0], np.cumsum(p)])
+        R = ex.kept[b]
+        assert excl[R - 1] <= wl.top_p + 1e-9
+        assert excl[R] > wl.top_p - 1e-9
+
+
+def test_status_rows():
+    V = 64
+    X = np.zeros((7, V), np.float32)
+    X[0, 3] = np.nan
+    X[1, 4] = np.inf
+    mask = np.full((7, 2), 0xFFFFFFFF, np.uint32)
+    mask[2] = 0  # nothing allowed
+    mask[3] = 0
+    mask[3, 1] = 1 << 7  # only token 39
+    hist = np.full((7, 2), -1, np.int32)
+    hist[4, 1] = V  # out of range
+    u = np.full(7, 0.5, np.float32)
+    u[5] = 1.0
+    X[6] = -np.inf  # every allowed logit -inf
+    r = O.sample_rows(X, O.DTYPE_F32, temperature=1.0, repetition_penalty=1.2, history=hist,
+                      allow_mask=mask.view(np.int32), uniforms=u)
+    assert r.status.tolist() == [O.ROW_NONFINITE, O.ROW_NONFINITE, O.ROW_EMPTY, O.ROW_OK,
+                                 O.ROW_BAD_HISTORY, O.ROW_BAD_UNIFORM, O.ROW_EMPTY]
+    assert r.ids[3] == 39 and r.kept[3] == 1
+    assert (r.ids[[0, 1, 2, 4, 5, 6]] == -1).all()
+
+
+@pytest.mark.parametrize("top_p", [0.0, 1.0, 1.5, -0.2])
+def test_top_p_outside_open_interval_is_off(top_p):
+    rng = np.random.default_rng(6)
+    X = rng.standard_normal((4, 300)).astype(np.float32)
+    u = rng.random(4).astype(np.float32)
+    a = O.sample_rows(X, O.DTYPE_F32, temperature=1.0, top_p=top_p, uniforms=u)
+    b = O.sample_rows(X, O.DTYPE_F32, temperature=1.0, top_p=1.0, uniforms=u)
+    assert (a.ids == b.ids).all() and (a.kept == 300).all()
+
+
+def test_finished_rows_get_pad_id():
+    rng = np.random.default_rng(7)
+    X = rng.standard_normal((4, 50)).astype(np.float32)
+    fin = np.array([1, 0, 1, 0], np.uint8)
+    r = O.sample_rows(X, O.DTYPE_F32, temperature=0.0, finished=fin, pad_token_id=-7)
+    assert r.ids[0] == -7 and r.ids[2] == -7
+    assert r.ids[1] == int(np.argmax(X[1]))
