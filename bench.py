@@ -5,12 +5,20 @@ the sampler over a bf16 [256, 248320] batch (repetition penalty over a
 4096-token history, 8%-density allow mask, T 0.7, top-k 64, top-p 0.9) and
 one logprob/entropy pass over bf16 [8192, 248320] with int32 targets.
 Inputs are generated on the GPU and resident in HBM before timing; two
-sampler batches alternate so consecutive steps do not hit the 256 MB MALL
-(the 4 GB logprob pass between them evicts it as well).
+sampler batches alternate and the 4 GB logprob pass between them evicts the
+256 MB MALL, so every sampler launch reads its logits from HBM.
 
 Prints ONE JSON line.  ``value`` is sampled rows/s of the sampler kernel;
 ``logprob_tokens_per_s`` is the logprob kernel's throughput.  Kernel times
-come from HIP events around each launch on the launch stream.
+come from HIP events recorded around each launch on the stream the kernels
+are launched on (torch's current stream, which the ops use).
+
+``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
+[64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
+512 MB buffer written between launches to evict the MALL.
+
+``--calibrate-copy`` runs only a 1 GiB device-to-device copy (the reference
+kernel whose rocprof FETCH_SIZE / WRITE_SIZE scale the HBM traffic counters).
 """
 
 from __future__ import annotations
@@ -27,7 +35,7 @@ if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
 
-def cpu_baseline(wl_cpu, lx_cpu, lt_cpu):
+def cpu_baseline(wl_cpu, lx_cpu, lt_cpu, min_seconds: float = 10.0):
     """The reference's CPU path (oracle/cpu_reference.py), timed on a bounded
     sample of the same workload with all host threads."""
     import torch
@@ -37,22 +45,22 @@ def cpu_baseline(wl_cpu, lx_cpu, lt_cpu):
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
     torch.set_num_threads(threads)
-    rows = 32
-    x = wl_cpu.logits[:rows]
-    bits = W.unpack_mask(wl_cpu.allow_mask[:rows], x.shape[1])
+    rows = wl_cpu.logits.shape[0]
+    x = wl_cpu.logits
+    bits = W.unpack_mask(wl_cpu.allow_mask, x.shape[1])
     kw = dict(temperature=wl_cpu.temperature, top_k=wl_cpu.top_k, top_p=wl_cpu.top_p,
-              repetition_penalty=wl_cpu.repetition_penalty, history=wl_cpu.history[:rows],
-              allow_mask_bits=bits, uniforms=wl_cpu.uniforms[:rows])
+              repetition_penalty=wl_cpu.repetition_penalty, history=wl_cpu.history,
+              allow_mask_bits=bits, uniforms=wl_cpu.uniforms)
     CR.sample_rows(x, **kw)  # warmup
     reps, t0 = 0, time.perf_counter()
-    while reps < 5 or time.perf_counter() - t0 < 5.0:
+    while reps < 3 or time.perf_counter() - t0 < min_seconds:
         CR.sample_rows(x, **kw)
         reps += 1
     s_rows = rows * reps / (time.perf_counter() - t0)
     lrows = lx_cpu.shape[0]
     CR.logprob_entropy_rows(lx_cpu, lt_cpu)
     reps, t0 = 0, time.perf_counter()
-    while reps < 5 or time.perf_counter() - t0 < 5.0:
+    while reps < 3 or time.perf_counter() - t0 < min_seconds:
         CR.logprob_entropy_rows(lx_cpu, lt_cpu)
         reps += 1
     l_tok = lrows * reps / (time.perf_counter() - t0)
@@ -61,9 +69,56 @@ def cpu_baseline(wl_cpu, lx_cpu, lt_cpu):
         "unit": "rows/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"sampler: {rows} rows of the bf16 [256, 248320] batch, full V; "
-                  f"logprob: {lrows} rows of [8192, 248320] -> {l_tok:.1f} tokens/s",
+        "sample": f"sampler: {rows} rows of the bf16 [256, 248320] batch (same penalty, mask, "
+                  f"T, top-k, top-p), full V, >= {min_seconds:.0f} s; logprob: {lrows} rows of "
+                  f"bf16 [8192, 248320] -> {l_tok:.1f} tokens/s",
         "logprob_tokens_per_s": round(l_tok, 2),
+    }
+
+
+def calibrate_copy(iters: int = 5) -> None:
+    """1 GiB device-to-device copies: FETCH_SIZE and WRITE_SIZE of this kernel
+    should each read 1 GiB = 1048576 KiB per dispatch."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "iters": iters}), flush=True)
+
+
+def time_sampler_config(cfg: int, dev, iters: int, flush):
+    """Average kernel time of one sampler launch on workload ``cfg`` with the
+    MALL evicted before every launch."""
+    import torch
+
+    from graspo_amd import ops
+    from graspo_amd import workloads as W
+
+    wl = W.sampler_workload(cfg, device=dev)
+    kw = wl.kwargs()
+    for _ in range(2):
+        ops.sample(wl.logits, **kw)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for e0, e1 in evs:
+        flush.add_(1)
+        e0.record()
+        ops.sample(wl.logits, **kw)
+        e1.record()
+    torch.cuda.synchronize()
+    us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+    B = wl.logits.shape[0]
+    nbytes = wl.algorithmic_bytes()
+    return {
+        "shape": list(wl.logits.shape), "dtype": str(wl.logits.dtype).replace("torch.", ""),
+        "avg_us": round(us, 2), "rows_per_s": round(B / (us * 1e-6), 1),
+        "algorithmic_bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
     }
 
 
@@ -73,6 +128,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-config", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -81,6 +138,10 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return 0
 
     import graspo_amd
     from graspo_amd import ops
@@ -109,7 +170,6 @@ def main() -> int:
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -155,8 +215,18 @@ def main() -> int:
         "logprob_tokens_per_s": round(N / (l_ms * 1e-3), 1),
         "roofline": dominant,
         "rooflines": {"sampler": roof_s, "logprob": roof_l},
+        "per_config": None,
         "cpu_baseline": None,
     }
+    del lx, lt, batches, wl_b
+    if not args.no_per_config:
+        flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
+        line["per_config"] = {
+            f"sampler_{name}": time_sampler_config(cfg, dev, 20, flush)
+            for cfg, name in ((1, "fp32_8x151936"), (2, "bf16_64x151936_top_p"),
+                              (3, "bf16_64x151936_masked"))
+        }
+        del flush
     if not args.no_cpu_baseline:
         cw = W.sampler_workload(5, device="cpu", rows=32)
         clx, clt = W.logprob_workload(5, device="cpu", rows=64)

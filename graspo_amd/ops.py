@@ -35,6 +35,9 @@ class SampleOutput(NamedTuple):
 
 
 def _stream(t: torch.Tensor) -> int:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"graspo_tokpath: tensors must be on a GPU (got {t.device}); there is no CPU path")
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
