@@ -1,0 +1,237 @@
+// tokpath_stream.h -- the streaming core shared by the gfx950 token-path kernels.
+//
+// A row of logits is read once, as 16-byte vectors (8 bf16 / 8 fp16 / 4 fp32
+// elements), NG vectors per thread per step.  Steps are double-buffered in
+// registers: the loads of step i+1 are issued before step i is folded, so
+// every wave keeps NG x 16 bytes per lane in flight while its VALU work runs.
+// Everything here is force-inlined so the compiler sees global (not flat)
+// pointers and can count outstanding loads exactly.
+//
+// The per-element VALU budget is what bounds these kernels on MI355X: at
+// 8 TB/s a bf16 row delivers 4 G elements/s per TB/s... i.e. about 10 VALU
+// issue slots per element across the 256 CUs (v_exp_f32 alone takes 4).  The
+// fold below spends: 1 convert, 0.5 max (v_max3 on raw values, no
+// canonicalisation), 1 fma, 1 exp, 1 add (+2 for the entropy term).  NaN and
+// +inf are not tested per element: a NaN logit makes exp2(d) NaN and a +inf
+// logit makes d = inf - inf = NaN, so either poisons the running sum, which
+// the caller reports as a non-finite row.
+#pragma once
+
+#include "tokpath_common.h"
+
+namespace gtp {
+
+// native 4 x u32 vector (what a 16-byte global load returns)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// max of three floats without the IEEE canonicalisation the compiler inserts
+// around fmaxf of bit-cast values (v_max3_f32 ignores quiet NaN inputs; a NaN
+// row is caught through the sum instead).
+__device__ __forceinline__ float max3raw(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// One 16-byte vector of logits.
+template <typename T>
+struct Vec;
+
+template <>
+struct Vec<uint16_t> {  // bf16 bit patterns
+  static constexpr int kE = 8;
+  __device__ static __forceinline__ void cvt(const u32x4& v, float (&x)[8]) {
+    x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x);
+    x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
+    x[4] = bf16_lo(v.z); x[5] = bf16_hi(v.z);
+    x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
+  }
+};
+
+template <>
+struct Vec<_Float16> {
+  static constexpr int kE = 8;
+  __device__ static __forceinline__ void cvt(const u32x4& v, float (&x)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xFFFFu));
+      x[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
+    }
+  }
+};
+
+template <>
+struct Vec<float> {
+  static constexpr int kE = 4;
+  __device__ static __forceinline__ void cvt(const u32x4& v, float (&x)[4]) {
+    x[0] = u2f(v.x); x[1] = u2f(v.y); x[2] = u2f(v.z); x[3] = u2f(v.w);
+  }
+};
+
+// Maximum of an NG x E block of raw values (v_max3 chains).
+template <int NG, int E>
+__device__ __forceinline__ float block_max_raw(const float (&x)[NG][E]) {
+  constexpr int N = NG * E;  // >= 4
+  static_assert(N >= 4, "block too small");
+  float m = max3raw(x[0][0], x[0][1], x[0][2]);
+  // the flattened block, two values per v_max3
+#pragma unroll
+  for (int i = 3; i + 1 < N; i += 2) m = max3raw(m, x[i / E][i % E], x[(i + 1) / E][(i + 1) % E]);
+  if ((N - 3) & 1) m = max3raw(m, x[(N - 1) / E][(N - 1) % E], x[(N - 1) / E][(N - 1) % E]);
+  return m;
+}
+
+// Online log-sum-exp (+ entropy moment) of one thread, base-2 units:
+//   s = sum 2^{d_i},  t = sum 2^{d_i} d_i,  d_i = (x_i - m) log2(e).
+struct Lse3 {
+  float m;  // running max, natural units (-inf while nothing finite is seen)
+  float s;
+  float t;
+};
+
+// Fold a block of raw logits.  kEntropy selects whether t is kept.
+template <bool kEntropy, int NG, int E>
+__device__ __forceinline__ void lse_fold_block(Lse3& st, const float (&x)[NG][E]) {
+  const float cm = block_max_raw<NG, E>(x);
+  if (cm > st.m) {
+    if (st.s > 0.0f) {
+      const float dl = (st.m - cm) * kLog2e;
+      const float f = __builtin_amdgcn_exp2f(dl);
+      if (kEntropy) st.t = f * __builtin_fmaf(dl, st.s, st.t);
+      st.s *= f;
+    }
+    st.m = cm;
+  }
+  // all -inf so far: any finite base keeps d = -inf (weight 0) and NaN = NaN
+  const float mL = st.m == kNegInf ? 0.0f : st.m * kLog2e;
+  float s0 = 0.0f, s1 = 0.0f, t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NG; ++k) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const float d = __builtin_fmaf(x[k][j], kLog2e, -mL);
+      const float e = __builtin_amdgcn_exp2f(d);
+      if ((k * E + j) & 1) {
+        s1 += e;
+        if (kEntropy) t1 = __builtin_fmaf(e, fmaxf(d, -256.0f), t1);
+      } else {
+        s0 += e;
+        if (kEntropy) t0 = __builtin_fmaf(e, fmaxf(d, -256.0f), t0);
+      }
+    }
+  }
+  st.s += s0 + s1;
+  if (kEntropy) st.t += t0 + t1;
+}
+
+__device__ __forceinline__ Lse3 lse3_merge(Lse3 a, Lse3 b) {
+  if (a.s != a.s || b.s != b.s) return {fmaxf(a.m, b.m), __builtin_nanf(""), __builtin_nanf("")};
+  const float m = fmaxf(a.m, b.m);
+  if (m == kNegInf) return {kNegInf, 0.0f, 0.0f};
+  float s = 0.0f, t = 0.0f;
+  if (a.s > 0.0f) {
+    const float da = (a.m - m) * kLog2e;  // <= 0
+    const float fa = __builtin_amdgcn_exp2f(da);
+    s += a.s * fa;
+    t += fa * __builtin_fmaf(da, a.s, a.t);
+  }
+  if (b.s > 0.0f) {
+    const float db = (b.m - m) * kLog2e;
+    const float fb = __builtin_amdgcn_exp2f(db);
+    s += b.s * fb;
+    t += fb * __builtin_fmaf(db, b.s, b.t);
+  }
+  return {m, s, t};
+}
+
+__device__ __forceinline__ Lse3 wave_lse3(Lse3 v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Lse3 w{__shfl_xor(v.m, o, kWave), __shfl_xor(v.s, o, kWave), __shfl_xor(v.t, o, kWave)};
+    v = lse3_merge(v, w);
+  }
+  return v;
+}
+
+// Block-wide merge; every thread gets the result.  `red` holds 3 floats per
+// wave.  Callers sync before reusing `red`.
+template <int NT>
+__device__ __forceinline__ Lse3 block_lse3(Lse3 v, float (*red)[3]) {
+  v = wave_lse3(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (lane == 0) {
+    red[wid][0] = v.m;
+    red[wid][1] = v.s;
+    red[wid][2] = v.t;
+  }
+  __syncthreads();
+  Lse3 r{red[0][0], red[0][1], red[0][2]};
+#pragma unroll
+  for (int w = 1; w < NT / kWave; ++w) r = lse3_merge(r, Lse3{red[w][0], red[w][1], red[w][2]});
+  return r;
+}
+
+// Stream vectors [v0, v1) of a 16-byte aligned row; thread tid folds vectors
+// v0 + step*NT*NG + k*NT + tid.  `fold(x, vec_index, valid)` receives each
+// step's converted block; `valid` is false only on the last step, where
+// vectors past v1 arrive as copies of vector v1-1 and must be ignored by the
+// caller (vec_index >= v1).  Loads of the next step are issued before the
+// current step is folded.
+template <typename T, int NT, int NG, bool kNonTemporal, typename Fold>
+__device__ __forceinline__ void stream_vectors(const T* __restrict__ row, int64_t v0, int64_t v1,
+                                               Fold&& fold) {
+  constexpr int E = Vec<T>::kE;
+  const int64_t n = v1 - v0;
+  if (n <= 0) return;
+  // 32-bit byte offsets from a uniform base: rows are far below 4 GB, and the
+  // saddr + voffset load form needs no 64-bit address arithmetic per vector
+  const char* __restrict__ base = reinterpret_cast<const char*>(row) + v0 * 16;
+  constexpr uint32_t kStep = (uint32_t)NT * NG;
+  const uint32_t nsteps = (uint32_t)((n + kStep - 1) / kStep);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t last = (uint32_t)(n - 1);
+  u32x4 a[NG], b[NG];
+  auto issue = [&](u32x4(&buf)[NG], uint32_t step) {
+    const uint32_t first = step * kStep + tid;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      uint32_t vi = first + (uint32_t)k * NT;
+      vi = vi < last ? vi : last;
+      const u32x4* p = reinterpret_cast<const u32x4*>(base + vi * 16u);
+      if (kNonTemporal)
+        buf[k] = __builtin_nontemporal_load(p);
+      else
+        buf[k] = *p;
+    }
+  };
+  auto consume = [&](const u32x4(&buf)[NG], uint32_t step) {
+    float x[NG][E];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
+    fold(x, v0 + (int64_t)(step * kStep + tid), step == nsteps - 1);
+  };
+  // Two steps per trip with one back-edge; prefetches past the last step
+  // re-load the last step's (cached) addresses instead of branching, so the
+  // outstanding-load count is the same on every path.
+  issue(a, 0);
+  for (uint32_t step = 0; step < nsteps; step += 2) {
+    issue(b, step + 1 < nsteps ? step + 1 : nsteps - 1);
+    consume(a, step);
+    issue(a, step + 2 < nsteps ? step + 2 : nsteps - 1);
+    if (step + 1 < nsteps) consume(b, step + 1);
+  }
+}
+
+// Mark the vectors of a block that lie past the end (only on the last step).
+template <int NG, int E, int NT>
+__device__ __forceinline__ void mask_tail(float (&x)[NG][E], int64_t vbase, int64_t v1) {
+#pragma unroll
+  for (int k = 0; k < NG; ++k)
+    if (vbase + (int64_t)k * NT >= v1) {
+#pragma unroll
+      for (int j = 0; j < E; ++j) x[k][j] = kNegInf;
+    }
+}
+
+}  // namespace gtp
