@@ -35,7 +35,7 @@
 //
 // Replaces _next_token_from_logits / _sample_next_token
 // (src/graspo/backends/graspoflow/tensor_utils.py:649-683).
-#include "tokpath_common.h"
+#include "tokpath_sampler_internal.h"
 
 namespace gtp {
 
@@ -50,30 +50,6 @@ constexpr int kNB = 2048;           // general-path bins
 constexpr float kBinScale = 64.0f;  // bins per nat
 constexpr int kCollectCap = 2048;
 
-struct SamplerArgs {
-  const void* logits;
-  int64_t V;
-  int64_t row_stride;
-  const int32_t* hist;
-  int64_t hist_len;
-  int64_t hist_stride;
-  const uint32_t* mask;
-  int64_t mask_stride;
-  const float* uniforms;
-  float T;
-  int32_t K;
-  float P;
-  float rho;
-  const uint8_t* finished;
-  int64_t pad_id;
-  int64_t* out_ids;
-  float* out_lp;
-  float* out_slp;
-  int32_t* out_kept;
-  float* out_tv;
-  int32_t* out_tid;
-  int32_t* out_status;
-};
 
 struct GeneralSmem {
   uint32_t ccum[kNB];            // bin counts, then inclusive prefix
@@ -410,7 +386,7 @@ __device__ RadixResult radix_search(SamplerSmem& sm, const Row<T>& r, float m, b
 // ---------------------------------------------------------------- kernel
 
 template <typename T>
-__global__ __launch_bounds__(kSB) void sampler_kernel(SamplerArgs a) {
+__global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
   __shared__ SamplerSmem sm;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
@@ -907,61 +883,26 @@ __global__ __launch_bounds__(kSB) void sampler_kernel(SamplerArgs a) {
 
 using namespace gtp;
 
-extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
-                               int64_t row_stride, const int32_t* history, int64_t hist_len,
-                               int64_t hist_stride, const uint32_t* allow_mask, int64_t mask_stride,
-                               const float* uniforms, const gtp_sampler_params* params,
-                               const uint8_t* finished, int64_t pad_token_id, int64_t* out_ids,
-                               float* out_logprob, float* out_sampled_logprob, int32_t* out_kept,
-                               float* out_thresh_value, int32_t* out_thresh_id, int32_t* out_status,
-                               void* stream) {
-  if (!params || B < 0 || V <= 0 || row_stride < V) return GTP_ERR_INVALID_ARGUMENT;
-  if (B > 0 && (!logits || !out_ids)) return GTP_ERR_INVALID_ARGUMENT;
-  if (!(params->repetition_penalty > 0.0f)) return GTP_ERR_INVALID_ARGUMENT;
-  if (allow_mask && mask_stride < (V + 31) / 32) return GTP_ERR_INVALID_ARGUMENT;
-  if (history && hist_len > 0 && hist_stride < hist_len) return GTP_ERR_INVALID_ARGUMENT;
-  if (hist_len < 0) return GTP_ERR_INVALID_ARGUMENT;
-  const bool greedy = !(params->temperature > 0.0f);
-  if (!greedy && !uniforms) return GTP_ERR_INVALID_ARGUMENT;
-  if (V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
-  if (B == 0) return GTP_OK;
-  SamplerArgs a;
-  a.logits = logits;
-  a.V = V;
-  a.row_stride = row_stride;
-  a.hist = history;
-  a.hist_len = history ? hist_len : 0;
-  a.hist_stride = hist_stride;
-  a.mask = allow_mask;
-  a.mask_stride = mask_stride;
-  a.uniforms = uniforms;
-  a.T = params->temperature;
-  a.K = params->top_k;
-  a.P = params->top_p;
-  a.rho = params->repetition_penalty;
-  a.finished = finished;
-  a.pad_id = pad_token_id;
-  a.out_ids = out_ids;
-  a.out_lp = out_logprob;
-  a.out_slp = out_sampled_logprob;
-  a.out_kept = out_kept;
-  a.out_tv = out_thresh_value;
-  a.out_tid = out_thresh_id;
-  a.out_status = out_status;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+namespace gtp {
+
+// One workgroup of 1024 threads per row; handles every row layout, vocabulary
+// and parameter combination the contract allows.
+int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s) {
   const dim3 grid((unsigned)B), block(kSB);
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      hipLaunchKernelGGL(sampler_kernel<uint16_t>, grid, block, 0, s, a);
+      hipLaunchKernelGGL(sampler_rowwise_kernel<uint16_t>, grid, block, 0, s, a);
       break;
     case GTP_DTYPE_F16:
-      hipLaunchKernelGGL(sampler_kernel<_Float16>, grid, block, 0, s, a);
+      hipLaunchKernelGGL(sampler_rowwise_kernel<_Float16>, grid, block, 0, s, a);
       break;
     case GTP_DTYPE_F32:
-      hipLaunchKernelGGL(sampler_kernel<float>, grid, block, 0, s, a);
+      hipLaunchKernelGGL(sampler_rowwise_kernel<float>, grid, block, 0, s, a);
       break;
     default:
       return GTP_ERR_INVALID_ARGUMENT;
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }
+
+}  // namespace gtp

@@ -7,9 +7,10 @@
 // Everything here is force-inlined so the compiler sees global (not flat)
 // pointers and can count outstanding loads exactly.
 //
-// The per-element VALU budget is what bounds these kernels on MI355X: at
-// 8 TB/s a bf16 row delivers 4 G elements/s per TB/s... i.e. about 10 VALU
-// issue slots per element across the 256 CUs (v_exp_f32 alone takes 4).  The
+// The per-element VALU budget is what bounds these kernels on MI355X: 8 TB/s
+// of bf16 is 4 T elements/s, against about 39 T VALU lane-slots/s (256 CUs x
+// 64 lanes x 2.4 GHz), i.e. about 10 issue slots per element (v_exp_f32 alone
+// takes 4).  The
 // fold below spends: 1 convert, 0.5 max (v_max3 on raw values, no
 // canonicalisation), 1 fma, 1 exp, 1 add (+2 for the entropy term).  NaN and
 // +inf are not tested per element: a NaN logit makes exp2(d) NaN and a +inf
@@ -90,10 +91,10 @@ struct Lse3 {
   float t;
 };
 
-// Fold a block of raw logits.  kEntropy selects whether t is kept.
+// Fold a block of raw logits whose maximum is cm (NaN values aside).
+// kEntropy selects whether t is kept.
 template <bool kEntropy, int NG, int E>
-__device__ __forceinline__ void lse_fold_block(Lse3& st, const float (&x)[NG][E]) {
-  const float cm = block_max_raw<NG, E>(x);
+__device__ __forceinline__ void lse_fold_block_max(Lse3& st, const float (&x)[NG][E], float cm) {
   if (cm > st.m) {
     if (st.s > 0.0f) {
       const float dl = (st.m - cm) * kLog2e;
@@ -123,6 +124,11 @@ __device__ __forceinline__ void lse_fold_block(Lse3& st, const float (&x)[NG][E]
   }
   st.s += s0 + s1;
   if (kEntropy) st.t += t0 + t1;
+}
+
+template <bool kEntropy, int NG, int E>
+__device__ __forceinline__ void lse_fold_block(Lse3& st, const float (&x)[NG][E]) {
+  lse_fold_block_max<kEntropy, NG, E>(st, x, block_max_raw<NG, E>(x));
 }
 
 __device__ __forceinline__ Lse3 lse3_merge(Lse3 a, Lse3 b) {
@@ -172,18 +178,37 @@ __device__ __forceinline__ Lse3 block_lse3(Lse3 v, float (*red)[3]) {
   return r;
 }
 
+struct NoPrologue {
+  __device__ __forceinline__ void operator()() const {}
+};
+
 // Stream vectors [v0, v1) of a 16-byte aligned row; thread tid folds vectors
-// v0 + step*NT*NG + k*NT + tid.  `fold(x, vec_index, valid)` receives each
-// step's converted block; `valid` is false only on the last step, where
-// vectors past v1 arrive as copies of vector v1-1 and must be ignored by the
-// caller (vec_index >= v1).  Loads of the next step are issued before the
+// v0 + step*NT*NG + k*NT + tid.  `fold(x, sw, vec_index, last)` receives each
+// step's converted block; on the last step (last == true) vectors past v1
+// arrive as copies of vector v1-1 and must be ignored by the caller
+// (vec_index + k*NT >= v1).  Loads of the next step are issued before the
 // current step is folded.
-template <typename T, int NT, int NG, bool kNonTemporal, typename Fold>
-__device__ __forceinline__ void stream_vectors(const T* __restrict__ row, int64_t v0, int64_t v1,
-                                               Fold&& fold) {
+//
+// With kSide, vector v (absolute index) also loads side[v >> side_shift] in
+// the same pipeline (e.g. the allow-mask word that holds its bits); sw[k] is
+// that word (0xFFFFFFFF without kSide).
+//
+// `prologue()` runs once, after the first step's loads are issued: set-up
+// work whose own loads then overlap the stream's first round trip.  It is
+// called by every thread, also when the range is empty.
+template <typename T, int NT, int NG, bool kNonTemporal, bool kSide, typename Fold,
+          typename Prologue = NoPrologue>
+__device__ __forceinline__ void stream_vectors_side(const T* __restrict__ row, int64_t v0,
+                                                    int64_t v1,
+                                                    const uint32_t* __restrict__ side,
+                                                    int side_shift, Fold&& fold,
+                                                    Prologue&& prologue = Prologue{}) {
   constexpr int E = Vec<T>::kE;
   const int64_t n = v1 - v0;
-  if (n <= 0) return;
+  if (n <= 0) {
+    prologue();
+    return;
+  }
   // 32-bit byte offsets from a uniform base: rows are far below 4 GB, and the
   // saddr + voffset load form needs no 64-bit address arithmetic per vector
   const char* __restrict__ base = reinterpret_cast<const char*>(row) + v0 * 16;
@@ -192,7 +217,8 @@ __device__ __forceinline__ void stream_vectors(const T* __restrict__ row, int64_
   const uint32_t tid = threadIdx.x;
   const uint32_t last = (uint32_t)(n - 1);
   u32x4 a[NG], b[NG];
-  auto issue = [&](u32x4(&buf)[NG], uint32_t step) {
+  uint32_t sa[NG], sb[NG];
+  auto issue = [&](u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t step) {
     const uint32_t first = step * kStep + tid;
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
@@ -203,23 +229,113 @@ __device__ __forceinline__ void stream_vectors(const T* __restrict__ row, int64_
         buf[k] = __builtin_nontemporal_load(p);
       else
         buf[k] = *p;
+      if (kSide) sbuf[k] = side[(uint64_t)(v0 + vi) >> side_shift];
     }
   };
-  auto consume = [&](const u32x4(&buf)[NG], uint32_t step) {
+  auto consume = [&](const u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t step) {
     float x[NG][E];
 #pragma unroll
-    for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
-    fold(x, v0 + (int64_t)(step * kStep + tid), step == nsteps - 1);
+    for (int k = 0; k < NG; ++k) {
+      Vec<T>::cvt(buf[k], x[k]);
+      if (!kSide) sbuf[k] = 0xFFFFFFFFu;
+    }
+    fold(x, sbuf, v0 + (int64_t)(step * kStep + tid), step == nsteps - 1);
   };
   // Two steps per trip with one back-edge; prefetches past the last step
   // re-load the last step's (cached) addresses instead of branching, so the
   // outstanding-load count is the same on every path.
-  issue(a, 0);
+  issue(a, sa, 0);
+  prologue();
   for (uint32_t step = 0; step < nsteps; step += 2) {
-    issue(b, step + 1 < nsteps ? step + 1 : nsteps - 1);
-    consume(a, step);
-    issue(a, step + 2 < nsteps ? step + 2 : nsteps - 1);
-    if (step + 1 < nsteps) consume(b, step + 1);
+    issue(b, sb, step + 1 < nsteps ? step + 1 : nsteps - 1);
+    consume(a, sa, step);
+    issue(a, sa, step + 2 < nsteps ? step + 2 : nsteps - 1);
+    if (step + 1 < nsteps) consume(b, sb, step + 1);
+  }
+}
+
+// The same without side words: fold(x, vec_index, last).
+template <typename T, int NT, int NG, bool kNonTemporal, typename Fold,
+          typename Prologue = NoPrologue>
+__device__ __forceinline__ void stream_vectors(const T* __restrict__ row, int64_t v0, int64_t v1,
+                                               Fold&& fold, Prologue&& prologue = Prologue{}) {
+  constexpr int E = Vec<T>::kE;
+  stream_vectors_side<T, NT, NG, kNonTemporal, false>(
+      row, v0, v1, nullptr, 0,
+      [&](float(&x)[NG][E], const uint32_t(&)[NG], int64_t vbase, bool last) {
+        fold(x, vbase, last);
+      },
+      prologue);
+}
+
+// Per-wave dynamic variant.  The range is cut into chunks of 64 * NG vectors;
+// each wave takes the next chunk from an LDS counter (`*counter` must be 0
+// and visible to every wave before the call), so waves that the scheduler
+// favours simply take more chunks and all waves of the workgroup finish
+// together.  Lane l of a wave folds vectors chunk*64*NG + k*64 + l.
+// `fold(x, sw, vec_index, last)`: vector k of the block is vec_index + k*64;
+// when `last`, indices >= v1 are copies to be ignored.  After the range is
+// exhausted a wave's prefetch loads one cached vector instead of branching.
+template <typename T, int NG, bool kNonTemporal, bool kSide, typename Fold,
+          typename Prologue = NoPrologue>
+__device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, int64_t v0,
+                                                   int64_t v1, const uint32_t* __restrict__ side,
+                                                   int side_shift, uint32_t* counter, Fold&& fold,
+                                                   Prologue&& prologue = Prologue{}) {
+  constexpr int E = Vec<T>::kE;
+  constexpr uint32_t kChunk = (uint32_t)kWave * NG;
+  const int64_t n = v1 - v0;
+  if (n <= 0) {
+    prologue();
+    return;
+  }
+  const char* __restrict__ base = reinterpret_cast<const char*>(row) + v0 * 16;
+  const uint32_t nchunks = (uint32_t)((n + kChunk - 1) / kChunk);
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const uint32_t last = (uint32_t)(n - 1);
+  auto grab = [&]() -> uint32_t {
+    uint32_t c = 0;
+    if (lane == 0) c = atomicAdd(counter, 1u);
+    return __builtin_amdgcn_readfirstlane(c);
+  };
+  u32x4 a[NG], b[NG];
+  uint32_t sa[NG], sb[NG];
+  auto issue = [&](u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t chunk) {
+    const bool live = chunk < nchunks;
+    const uint32_t first = chunk * kChunk + lane;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      uint32_t vi = first + (uint32_t)k * kWave;
+      vi = vi < last ? vi : last;
+      vi = live ? vi : 0u;
+      const u32x4* p = reinterpret_cast<const u32x4*>(base + vi * 16u);
+      if (kNonTemporal)
+        buf[k] = __builtin_nontemporal_load(p);
+      else
+        buf[k] = *p;
+      if (kSide) sbuf[k] = side[(uint64_t)(v0 + vi) >> side_shift];
+    }
+  };
+  auto consume = [&](const u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t chunk) {
+    float x[NG][E];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      Vec<T>::cvt(buf[k], x[k]);
+      if (!kSide) sbuf[k] = 0xFFFFFFFFu;
+    }
+    fold(x, sbuf, v0 + (int64_t)(chunk * kChunk + lane), chunk == nchunks - 1);
+  };
+  uint32_t ca = grab();
+  issue(a, sa, ca);
+  prologue();
+  while (ca < nchunks) {
+    const uint32_t cb = grab();
+    issue(b, sb, cb);
+    consume(a, sa, ca);
+    if (cb >= nchunks) break;
+    ca = grab();
+    issue(a, sa, ca);
+    consume(b, sb, cb);
   }
 }
 

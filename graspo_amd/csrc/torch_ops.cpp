@@ -9,7 +9,10 @@
 #include <ATen/ATen.h>
 #include <torch/library.h>
 
+#include <map>
+#include <mutex>
 #include <tuple>
+#include <utility>
 
 #include "graspo_tokpath.h"
 
@@ -51,6 +54,22 @@ int64_t row_stride_of(const at::Tensor& logits) {
 
 void check_same_device(const at::Tensor& a, const at::Tensor& b, const char* name) {
   TORCH_CHECK(b.device() == a.device(), "graspo_tokpath: ", name, " must be on ", a.device());
+}
+
+// Sampler workspace, one per (device, stream): zero-filled when allocated (the
+// library keeps it reusable from call to call), grown when a call needs more.
+// Calls on one stream are ordered, so they can share it.
+void* sampler_workspace(const at::Tensor& like, size_t bytes, int64_t stream) {
+  if (bytes == 0) return nullptr;
+  static std::mutex mu;
+  static std::map<std::pair<int, int64_t>, at::Tensor> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  at::Tensor& ws = cache[{(int)like.get_device(), stream}];
+  if (!ws.defined() || (size_t)ws.numel() < bytes) {
+    const int64_t n = (int64_t)((bytes + 4095) / 4096 * 4096);
+    ws = at::zeros({n}, like.options().dtype(at::kByte));
+  }
+  return ws.data_ptr();
 }
 
 using SampleOut =
@@ -123,11 +142,14 @@ SampleOut sample(const at::Tensor& logits, double temperature, int64_t top_k, do
   p.top_k = (int32_t)top_k;
   p.top_p = (float)top_p;
   p.repetition_penalty = (float)repetition_penalty;
+  const size_t ws_bytes = gtp_sample_workspace_bytes(dtype_code(logits), B, V, &p);
+  void* ws = sampler_workspace(logits, ws_bytes, stream);
   const int rc = gtp_sample_rows(
       logits.data_ptr(), dtype_code(logits), B, V, row_stride_of(logits), hist, hist_len,
       hist_stride, mask, mask_stride, u, &p, fin, pad_token_id, ids.data_ptr<int64_t>(),
       lp.data_ptr<float>(), slp.data_ptr<float>(), kept.data_ptr<int32_t>(), tv.data_ptr<float>(),
-      tid.data_ptr<int32_t>(), st.data_ptr<int32_t>(), reinterpret_cast<void*>(stream));
+      tid.data_ptr<int32_t>(), st.data_ptr<int32_t>(), ws, ws_bytes,
+      reinterpret_cast<void*>(stream));
   check_rc(rc, "gtp_sample_rows");
   return {ids, lp, slp, kept, tv, tid, st};
 }

@@ -115,6 +115,11 @@ typedef struct gtp_sampler_params {
  *               pad_token_id as their id (the where() of
  *               _broadcast_and_pad_finished, tensor_utils.py:661-668)
  *   outputs     [B] each; any of them may be NULL except out_ids.
+ *   workspace   device scratch of at least gtp_sample_workspace_bytes()
+ *               bytes (may be NULL when that is 0), 256-byte aligned,
+ *               zero-filled once when allocated.  Calls leave it ready for
+ *               the next call; two calls that may run at the same time
+ *               (e.g. on different streams) need different workspaces.
  */
 int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
                     int64_t row_stride, const int32_t* history, int64_t hist_len,
@@ -124,7 +129,18 @@ int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
                     int64_t pad_token_id, int64_t* out_ids, float* out_logprob,
                     float* out_sampled_logprob, int32_t* out_kept,
                     float* out_thresh_value, int32_t* out_thresh_id,
-                    int32_t* out_status, void* stream);
+                    int32_t* out_status, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * gtp_sample_workspace_bytes -- workspace gtp_sample_rows needs for B rows of
+ * V logits of `dtype` under `params` (0 when the call needs none).  Greedy and
+ * top-k rows (1 <= top_k <= 128) split each row over several workgroups and
+ * merge per-row candidate lists through the workspace; other calls run one
+ * workgroup per row and need none.
+ */
+size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
+                                  const gtp_sampler_params* params);
 
 /*
  * gtp_logprob_entropy_rows -- log_softmax(x)[target] and softmax entropy per
