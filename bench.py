@@ -31,6 +31,9 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 REPO = os.path.dirname(os.path.abspath(__file__))
+SAMPLER_KERNEL = "sampler_split_kernel<bf16>"
+LOGPROB_KERNEL = "logprob_entropy_kernel<bf16>"
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_large_vocab.md")
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
@@ -74,6 +77,22 @@ def cpu_baseline(wl_cpu, lx_cpu, lt_cpu, min_seconds: float = 10.0):
                   f"bf16 [8192, 248320] -> {l_tok:.1f} tokens/s",
         "logprob_tokens_per_s": round(l_tok, 2),
     }
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` as measured by rocprofv3 FETCH_SIZE
+    and WRITE_SIZE counters (scaled by the copy-kernel calibration), read from
+    the committed profile summary's ``traffic_bytes <kernel> <bytes>`` lines.
+    None when no such line exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                parts = ln.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def calibrate_copy(iters: int = 5) -> None:
@@ -185,12 +204,12 @@ def main() -> int:
     s_gbs = s_bytes / (s_ms * 1e-3) / 1e9
     l_gbs = l_bytes / (l_ms * 1e-3) / 1e9
     roof_s = {"bound": "hbm", "achieved": round(s_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-              "frac": round(s_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-              "kernel": "sampler_kernel<bf16>", "algorithmic_bytes": s_bytes,
+              "frac": round(s_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(SAMPLER_KERNEL),
+              "kernel": SAMPLER_KERNEL, "algorithmic_bytes": s_bytes,
               "avg_us": round(s_ms * 1e3, 2)}
     roof_l = {"bound": "hbm", "achieved": round(l_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-              "frac": round(l_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-              "kernel": "logprob_entropy_kernel<bf16>", "algorithmic_bytes": l_bytes,
+              "frac": round(l_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(LOGPROB_KERNEL),
+              "kernel": LOGPROB_KERNEL, "algorithmic_bytes": l_bytes,
               "avg_us": round(l_ms * 1e3, 2)}
     dominant = roof_l if l_ms >= s_ms else roof_s
     line = {
