@@ -3,47 +3,48 @@
 //
 // One workgroup of 1024 threads per CU.  A row is split into S slices
 // (S = ceil(CUs / B), so a B >= 256 batch is one row per workgroup and every
-// workgroup of the launch is resident at once): all slices stream together,
-// and the selection tails run after the memory system has drained.
+// workgroup of the launch is resident at once).
 //
-// 1. Stream (the only HBM read of the slice; tokpath_stream.h).  Per step a
-//    wave takes the next chunk of 64 x 5 vectors (8 bf16/fp16 or 4 fp32
-//    logits each) from an LDS counter, so all waves finish together, and
-//    folds it into an online log-sum-exp of the raw logits (the logprob output) and writes,
-//    per vector, a 16-bit order key of its raw maximum rounded up to bf16
-//    into LDS.  The slice's allow-mask words are staged in LDS by the stream
-//    prologue; a vector with no allowed token gets key 0 and is never looked
-//    at again.  History ids are loaded in the prologue and set the slice's
-//    penalty bitmap (LDS) after the stream.
-// 2. Select.  A processed logit is never above the processed value of its
-//    vector's key: the penalty lowers logits when rho >= 1 (for rho < 1 the
-//    bound is raised to match), and division by the temperature is monotone.
-//    So for a key threshold tau, every token of a vector with key < tau has
-//    y <= Y_out = bound(key tau-1).  tau comes from a 256-bin LDS histogram
-//    of the keys, sized so that about k / (allowed density) vectors pass; only
-//    those vectors are re-read (L2), their tokens get the exact penalty, mask
-//    and IEEE division by the temperature, and those with y > Y_out are kept.
-//    Once at least k such tokens exist, the slice's top-k (by y desc, id asc)
-//    is among them; otherwise tau is moved using the measured hit rate, and
-//    finally every vector is taken.  The top k of the kept tokens are ranked
-//    by counting (<= 256 tokens) or an 8-bit radix select on the 64-bit
-//    (y, id) key (re-reading the passing vectors per digit if more than 1024
-//    tokens pass, e.g. under massive exact ties).
-// 3. With S == 1 the workgroup finishes the row from LDS.  Otherwise it
+// 1. Pilot.  Each thread first loads 4 vectors (8 bf16/fp16 or 4 fp32 logits
+//    each) from the start of the slice -- before any other load, so they
+//    come back first -- and takes the largest allowed one, lowered by the
+//    largest possible penalty.  Each wave sorts its 64 values in registers
+//    and posts its top 16; the last wave to post picks the Kc-th largest,
+//    theta1.  Those values belong to distinct tokens, so at least Kc allowed
+//    tokens have a penalised logit >= theta1.  No block barrier is involved:
+//    a wave issues its first stream chunks as soon as it has posted, and
+//    only waits for theta with those loads in flight.
+// 2. Stream (the only HBM read of the slice; tokpath_stream.h).  Waves take
+//    chunks of 64 x 4 vectors from an LDS counter (the allow-mask word of
+//    each vector travels with it) and fold them into an online log-sum-exp
+//    of the raw logits (the logprob output).  Every allowed token with
+//    x >= theta (theta1 mapped back through the penalty's largest increase
+//    and lowered by 2^-12) is captured into an LDS pool of (id, x); a lane
+//    whose block maximum is below theta pays one compare.  History ids set
+//    a penalty bitmap in LDS while the first chunks are in flight.
+// 3. Resolve.  The pooled tokens get the exact penalty, mask and IEEE
+//    division by the temperature.  A token left out has x < theta, so its
+//    processed logit is <= ub(theta); when at least Kc pooled tokens beat
+//    that bound, the slice's top Kc (by y desc, id asc) is among them.  A
+//    1024-bin histogram of 16-bit keys (wave 0 finds the Kc-th) trims the
+//    pool before ranking by counting (<= 256 tokens) or an 8-bit radix select
+//    on the 64-bit (y, id) key.  When the pool overflowed or does not
+//    separate (e.g. massive exact ties), the slice falls back to per-vector
+//    keys re-read from HBM and a threshold search over them.
+// 4. With S == 1 the workgroup finishes the row from LDS.  Otherwise it
 //    publishes its sorted top-k and (m, s) to the workspace and the last
-//    workgroup of the row to arrive (an epoch-tagged counter advanced with
-//    compare-and-swap, so no workgroup ever waits on another) merges the S
+//    workgroup of the row to arrive (a per-row counter in the workspace,
+//    which that workgroup returns to zero, so no workgroup ever waits on
+//    another and the workspace is ready for the next call) merges the S
 //    lists by binary-search ranks.
-// 4. Finish: fixed-point weights (DETEXP_FIX), exact top-p cut and
-//    inverse-CDF draw over the sorted top-k, outputs.
+// 5. Finish (one wave): fixed-point weights (DETEXP_FIX), exact top-p cut
+//    and inverse-CDF draw over the sorted top-k, counted with ballots.
 //
 // Every output follows the contract of include/graspo_tokpath.h bit for bit;
 // the threshold logic only decides which tokens are evaluated exactly.
 //
 // Replaces _next_token_from_logits / _sample_next_token
 // (src/graspo/backends/graspoflow/tensor_utils.py:649-683).
-#include <atomic>
-
 #include "tokpath_sampler_internal.h"
 #include "tokpath_stream.h"
 
@@ -51,10 +52,17 @@ namespace gtp {
 
 constexpr int kFT = 1024;                   // threads per workgroup (one per CU)
 constexpr int kFWaves = kFT / kWave;
-constexpr int kFG = 5;                      // vectors per thread per stream step
+constexpr int kTT = 256;                    // threads of the ranking tail (one wave per SIMD)
+constexpr int kFG = 4;                      // vectors per thread per stream step
 constexpr int kSliceVecs = 32768;           // most vectors in one slice (2^18 bf16 tokens)
 constexpr int kFastK = 128;                 // largest kept set of this path
-constexpr int kCand = 1024;                 // candidate slots (slice and merge)
+constexpr int kCand = 2048;                 // candidate slots of a slice (the capture pool)
+constexpr int kMergeCand = 1024;            // entries of all slice lists of a row
+constexpr int kPHist = 1024;                // bins of the final 16-bit key filter
+constexpr int kWTop = 16;                   // pilot keys each wave posts (its largest)
+// pilot vectors per thread (fp16 converts in more registers)
+template <typename T>
+constexpr int kNPof = Elem<T>::kDtype == GTP_DTYPE_F16 ? 3 : 4;
 constexpr int kSel = 2048;                  // re-read list entries per round
 constexpr int kPenWords = kSliceVecs * 8 / 32 + 2;
 constexpr int kMaxSlices = 64;
@@ -77,7 +85,6 @@ struct FastArgs {
   int64_t vps;            // vectors per slice
   unsigned char* ws;      // [B] counters (256-byte padded), then B * S slots
   size_t cnt_bytes;
-  uint32_t epoch;         // 1..65535, different for consecutive calls
   int32_t Kc;             // entries per slice list (1 when greedy)
   int32_t greedy;
   int32_t use_pen;
@@ -91,8 +98,7 @@ struct FastSmem {
     uint32_t soff[kMaxSlices + 1];   // merge: start of each slice's list in ckey / cx
   } u;
   uint32_t pen[kPenWords];           // penalty bitmap of the slice's tokens
-  uint32_t maskw[kPenWords];         // allow-mask words of the slice's tokens
-  unsigned long long ckey[kCand];    // candidates (slice), lists (merge)
+  unsigned long long ckey[kCand];    // capture pool / candidates (slice), lists (merge)
   float cx[kCand];
   uint16_t sel[kSel];
   unsigned long long skey[kFastK];   // the slice's survivors before sorting
@@ -101,10 +107,17 @@ struct FastSmem {
   float fx[kFastK];
   unsigned long long incl[kFastK];   // inclusive prefix of the fixed-point weights
   uint32_t hist[256];
+  uint32_t phist[kPHist];            // final filter histogram
+  uint32_t wtop[kFWaves * kWTop];    // each wave's largest pilot keys, descending
   float red[kFWaves][3];
   uint32_t redu[kFWaves];
   uint32_t redx[kFWaves][5];
   uint32_t ngt;
+  uint32_t pool_n;     // tokens captured during the stream
+  uint32_t kmax16;     // block maximum of 16-bit order keys (pilot, final filter)
+  uint32_t parrive;    // waves that have posted their pilot keys
+  uint32_t theta_ready;
+  uint32_t theta_bits; // the capture threshold, once theta_ready
   uint32_t chunk_ctr;  // next stream chunk (per-wave dynamic schedule)
   int32_t bucket;
   uint32_t above;
@@ -215,6 +228,81 @@ __device__ __forceinline__ void find_bucket(FastSmem& sm, uint32_t target) {
   }
 }
 
+// The calling wave (all 64 lanes): the bucket of an NB-bin histogram h (bin
+// NB-1 on top) that holds 0-based position `target`, or -1 when h holds no
+// more than `target` entries.  Returned to every lane.
+template <int NB>
+__device__ __forceinline__ int32_t wave_find_bucket(const uint32_t* h, uint32_t target,
+                                                   uint32_t* above_out = nullptr) {
+  constexpr int PL = NB / kWave;  // bins per lane, lane 0 holding the top ones
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t* hl = h + NB - PL * (lane + 1);  // this lane's bins, ascending
+  uint32_t tot = 0;
+#pragma unroll 8
+  for (int q = 0; q < PL; ++q) tot += hl[q];
+  uint32_t incl = tot;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t w = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += w;
+  }
+  const bool here = incl - tot <= target && target < incl;
+  const unsigned long long who = __ballot(here);
+  if (!who) return -1;
+  const int src = (int)__builtin_ctzll(who);
+  // the holding lane walks its bins from the top
+  int32_t bin = 0;
+  uint32_t ab = 0;
+  if (lane == src) {
+    uint32_t above = incl - tot;
+    for (int q = PL - 1; q >= 0; --q) {
+      const uint32_t cq = hl[q];
+      if (target < above + cq) {
+        bin = NB - PL * (lane + 1) + q;
+        ab = above;
+        break;
+      }
+      above += cq;
+    }
+  }
+  if (above_out) *above_out = (uint32_t)__shfl((int)ab, src, kWave);
+  return __shfl(bin, src, kWave);
+}
+
+// Sort the 64 R values of a wave in descending order in registers (bitonic
+// network; element r*64 + lane lives in v[r] of that lane).
+template <int R>
+__device__ __forceinline__ void wave_sort_desc(uint32_t (&v)[R]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int N = kWave * R;
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      if (j >= kWave) {
+        const int jr = j / kWave;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if ((r & jr) == 0) {
+            const bool desc = ((r * kWave + lane) & k) == 0;
+            const uint32_t hi = max(v[r], v[r | jr]), lo = min(v[r], v[r | jr]);
+            v[r] = desc ? hi : lo;
+            v[r | jr] = desc ? lo : hi;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t w = (uint32_t)__shfl_xor((int)v[r], j, kWave);
+          const bool desc = ((r * kWave + lane) & k) == 0;
+          const bool lower = (lane & j) == 0;
+          v[r] = desc == lower ? max(v[r], w) : min(v[r], w);
+        }
+      }
+    }
+  }
+}
+
 // Write one row's outputs (status != OK: id -1, or the pad id when finished).
 __device__ __forceinline__ void write_out(const SamplerArgs& a, int64_t b, int32_t status,
                                           int64_t id, float lp, float slp, int32_t kept, float tv,
@@ -249,9 +337,10 @@ struct Slice {
   int64_t V;
   uint32_t w0;           // first penalty word of the slice
 
-  __device__ __forceinline__ uint32_t mask_bits(const FastSmem& sm, int64_t e0, int n) const {
-    return mrow ? (sm.maskw[(uint32_t)(e0 >> 5) - w0] >> (e0 & 31)) & ((1u << n) - 1u)
-                : (1u << n) - 1u;
+  // allow bits of tokens [e0, e0 + n), n <= 8, inside one mask word (global
+  // read: only the rare paths look tokens up one by one)
+  __device__ __forceinline__ uint32_t mask_bits(int64_t e0, int n) const {
+    return mrow ? (mrow[e0 >> 5] >> (e0 & 31)) & ((1u << n) - 1u) : (1u << n) - 1u;
   }
   __device__ __forceinline__ uint32_t pen_bits(const FastSmem& sm, int64_t e0, int n) const {
     return (sm.pen[(uint32_t)(e0 >> 5) - w0] >> (e0 & 31)) & ((1u << n) - 1u);
@@ -320,7 +409,7 @@ __device__ __forceinline__ void emit_listed(const FastSmem& sm, const Slice<T>& 
     const int64_t vi = c.v0 + sm.sel[p];
     const u32x4 v = rv[vi];
     const int64_t e0 = vi * E;
-    const uint32_t mb = c.mask_bits(sm, e0, E);
+    const uint32_t mb = c.mask_bits(e0, E);
     const uint32_t pb = c.proc.use_pen ? c.pen_bits(sm, e0, E) : 0u;
     uint32_t cand = 0;
 #pragma unroll
@@ -340,7 +429,7 @@ template <typename T, typename F>
 __device__ __forceinline__ void emit_tail(const FastSmem& sm, const Slice<T>& c, float xout,
                                           float yout, F& f) {
   for (int64_t id = c.tail0 + threadIdx.x; id < c.V; id += kFT) {
-    if (!c.mask_bits(sm, id, 1)) continue;
+    if (!c.mask_bits(id, 1)) continue;
     const float x = Elem<T>::get(c.row, id);
     if (!(x > xout)) continue;
     const bool pen = c.proc.use_pen && c.pen_bits(sm, id, 1);
@@ -418,24 +507,25 @@ __device__ __forceinline__ void rank_sort_small(const unsigned long long* keys, 
 // per digit.  Rare: not executed on the common path.
 template <typename T>
 __device__ __forceinline__ void select_top_slow(FastSmem& sm, const Slice<T>& c, uint32_t ngt,
-                                             uint32_t Kc, uint32_t tau, float xout, float yout) {
+                                             uint32_t Kc, uint32_t tau, float xout, float yout,
+                                             int nthr) {
   const int tid = threadIdx.x;
   if (ngt <= (uint32_t)kCand) {
     const unsigned long long kth = radix_kth(
         sm, Kc,
         [&](unsigned long long prefix, unsigned long long pmask, int shift) {
-          for (uint32_t i = tid; i < ngt; i += kFT) {
+          for (uint32_t i = tid; tid < nthr && i < ngt; i += nthr) {
             const unsigned long long k = sm.ckey[i];
             if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFFu], 1u);
           }
         },
         [&](unsigned long long prefix, unsigned long long pmask) {
-          for (uint32_t i = tid; i < ngt; i += kFT)
+          for (uint32_t i = tid; tid < nthr && i < ngt; i += nthr)
             if ((sm.ckey[i] & pmask) == prefix) sm.found = sm.ckey[i];
         });
     if (tid == 0) sm.ngt = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < ngt; i += kFT) {
+    for (uint32_t i = tid; tid < nthr && i < ngt; i += nthr) {
       if (sm.ckey[i] >= kth) {
         const uint32_t slot = atomicAdd(&sm.ngt, 1u);
         sm.skey[slot] = sm.ckey[i];
@@ -472,15 +562,18 @@ __device__ __forceinline__ void select_top_slow(FastSmem& sm, const Slice<T>& c,
 }
 
 // Finish a row from its sorted top nk (sm.fkey / sm.fx): status, greedy pick
-// or fixed-point top-p cut and draw, outputs.  Block-uniform.
-__device__ __forceinline__ void finish_row(FastSmem& sm, const FastArgs& fa, int64_t b,
-                                        const Lse3& row_lse, bool bad_hist, uint32_t nk) {
+// or fixed-point top-p cut and draw, outputs.  Wave 0 only (lane r/2 holds
+// the weights of ranks r); the cut and the draw are counts of prefix sums
+// below a bound, taken with ballots.  Callers sync before (lists complete).
+__device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& fa, int64_t b,
+                                           float lm, float ls, bool bad_hist, uint32_t nk) {
   const SamplerArgs& a = fa.a;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x;
+  if (lane >= kWave) return;
   const float u = fa.greedy ? 0.0f : a.uniforms[b];
-  const float lse_raw = row_lse.m + __builtin_amdgcn_logf(row_lse.s) * kLn2;
+  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
   int32_t status = GTP_ROW_OK;
-  if (row_lse.s != row_lse.s || row_lse.m == kPosInf)
+  if (ls != ls || lm == kPosInf)
     status = GTP_ROW_NONFINITE;
   else if (bad_hist)
     status = GTP_ROW_BAD_HISTORY;
@@ -491,62 +584,44 @@ __device__ __forceinline__ void finish_row(FastSmem& sm, const FastArgs& fa, int
   else if (rank_key_y(sm.fkey[0]) == kPosInf)
     status = GTP_ROW_NONFINITE;
   if (status != GTP_ROW_OK) {
-    if (tid == 0) write_out(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
+    if (lane == 0) write_out(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
     return;
   }
   const unsigned long long k0 = sm.fkey[0];
   const float m = rank_key_y(k0);
   if (fa.greedy) {
-    if (tid == 0) {
+    if (lane == 0) {
       const int32_t id = rank_key_id(k0);
       write_out(a, b, GTP_ROW_OK, id, sm.fx[0] - lse_raw, 0.0f, 1, m, id);
     }
     return;
   }
-  // fixed-point weights and their inclusive prefix (wave 0, 2 ranks per lane)
-  if (tid < kWave) {
-    unsigned long long v[2], tot = 0;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t r = (uint32_t)tid * 2u + q;
-      v[q] = r < nk ? detexp_fix(rank_key_y(sm.fkey[r]) - m) : 0ull;
-      tot += v[q];
-    }
-    unsigned long long run = wave_incl_scan_u64(tot) - tot;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t r = (uint32_t)tid * 2u + q;
-      run += v[q];
-      if (r < nk) sm.incl[r] = run;
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned long long Wk = sm.incl[nk - 1];
-    int R = (int)nk;
-    if (fa.p_active) {
-      const unsigned long long F = floor_mul(a.P, Wk);
-      int lo = 0, hi = (int)nk - 1;  // R = 1 + #{r < nk-1 : incl[r] <= F}
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (sm.incl[mid] <= F) lo = mid + 1;
-        else hi = mid;
-      }
-      R = lo + 1;
-    }
-    const unsigned long long Wp = sm.incl[R - 1];
-    const unsigned long long U = floor_mul(u, Wp);
-    int lo = 0, hi = R - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (sm.incl[mid] <= U) lo = mid + 1;
-      else hi = mid;
-    }
-    const int rs = lo;
-    const unsigned long long ws = sm.incl[rs] - (rs ? sm.incl[rs - 1] : 0ull);
-    const unsigned long long kt = sm.fkey[R - 1];
-    const float slp = __builtin_amdgcn_logf((float)((double)ws / (double)Wp)) * kLn2;
-    write_out(a, b, GTP_ROW_OK, rank_key_id(sm.fkey[rs]), sm.fx[rs] - lse_raw, slp, R,
+  // fixed-point weights of ranks r0 = 2 lane, r1 = r0 + 1 and their
+  // inclusive prefix sums i0, i1
+  const uint32_t r0 = 2u * (uint32_t)lane, r1 = r0 + 1u;
+  const unsigned long long w0 = r0 < nk ? detexp_fix(rank_key_y(sm.fkey[r0]) - m) : 0ull;
+  const unsigned long long w1 = r1 < nk ? detexp_fix(rank_key_y(sm.fkey[r1]) - m) : 0ull;
+  const unsigned long long i1 = wave_incl_scan_u64(w0 + w1);
+  const unsigned long long i0 = i1 - w1;
+  auto incl_at = [&](uint32_t r) -> unsigned long long {  // r wave-uniform
+    const unsigned long long v = (r & 1u) ? i1 : i0;
+    return __shfl(v, (int)(r >> 1), kWave);
+  };
+  auto count_le = [&](uint32_t lim, unsigned long long bound) -> uint32_t {  // #{r < lim : incl[r] <= bound}
+    const unsigned long long c0 = __ballot(r0 < lim && i0 <= bound);
+    const unsigned long long c1 = __ballot(r1 < lim && i1 <= bound);
+    return (uint32_t)(__builtin_popcountll(c0) + __builtin_popcountll(c1));
+  };
+  const unsigned long long Wk = incl_at(nk - 1u);
+  const uint32_t R = fa.p_active ? 1u + count_le(nk - 1u, floor_mul(a.P, Wk)) : nk;
+  const unsigned long long Wp = incl_at(R - 1u);
+  const uint32_t rs = count_le(R - 1u, floor_mul(u, Wp));
+  const unsigned long long hi = incl_at(rs);
+  const unsigned long long lo = rs ? incl_at(rs - 1u) : 0ull;
+  if (lane == 0) {
+    const unsigned long long kt = sm.fkey[R - 1u];
+    const float slp = __builtin_amdgcn_logf((float)((double)(hi - lo) / (double)Wp)) * kLn2;
+    write_out(a, b, GTP_ROW_OK, rank_key_id(sm.fkey[rs]), sm.fx[rs] - lse_raw, slp, (int32_t)R,
               rank_key_y(kt), rank_key_id(kt));
   }
 }
@@ -557,15 +632,16 @@ __device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int6
   const int tid = threadIdx.x;
   const uint32_t Kc = (uint32_t)fa.Kc;
   const unsigned char* slots = fa.ws + fa.cnt_bytes + (size_t)b * S * kSlotBytes;
-  Lse3 part{kNegInf, 0.0f, 0.0f};
+  float lm = kNegInf, ls = 0.0f;
   uint32_t my_n = 0, my_flags = 0;
   if (tid < S) {
     const SliceHead* hj = reinterpret_cast<const SliceHead*>(slots + (size_t)tid * kSlotBytes);
-    part = Lse3{hj->m, hj->s, 0.0f};
+    lm = hj->m;
+    ls = hj->s;
     my_n = hj->n;
     my_flags = hj->flags;
   }
-  const Lse3 row_lse = block_lse3<kFT>(part, sm.red);
+  block_lse2<kFT>(lm, ls, sm.red);
   const bool any_bad_hist = __syncthreads_or(my_flags & 1u);
   uint32_t total;
   const uint32_t my_off = block_excl_scan(my_n, sm.redu, &total);
@@ -615,24 +691,26 @@ __device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int6
     }
   }
   __syncthreads();
-  finish_row(sm, fa, b, row_lse, any_bad_hist, nk);
+  finish_row(sm, fa, b, lm, ls, any_bad_hist, nk);
 }
 
 // --------------------------------------------------------------- the kernel
 
-template <typename T>
+template <typename T, bool kMask>
 __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   constexpr int E = Vec<T>::kE;
   constexpr int kHistPer = 4;  // history ids per thread per batch
+  constexpr int kNP = kNPof<T>;
   __shared__ FastSmem sm;
   const SamplerArgs& a = fa.a;
   const int tid = threadIdx.x;
   const int s = blockIdx.x, S = gridDim.x;
   const int64_t b = blockIdx.y;
+  const uint32_t Kc = (uint32_t)fa.Kc;
 
   Slice<T> c;
   c.row = reinterpret_cast<const T*>(a.logits) + b * a.row_stride;
-  c.mrow = a.mask ? a.mask + b * a.mask_stride : nullptr;
+  c.mrow = kMask ? a.mask + b * a.mask_stride : nullptr;
   c.proc = Proc{fa.greedy, fa.use_pen, a.rho, fa.Tc};
   c.V = a.V;
   const int64_t nvec = a.V / E;
@@ -646,48 +724,160 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   const int nw = (int)(((e1 - 1) >> 5) - (e0 >> 5) + 1);
   const bool read_hist = a.hist && a.hist_len > 0 && (fa.use_pen || s == 0);
   const int32_t* hrow = a.hist + b * a.hist_stride;
-  if (tid == 0) sm.chunk_ctr = 0u;
-  __syncthreads();
 
-  // ---- 0. (stream prologue) history ids into registers, penalty bitmap
-  // cleared; the bitmap is filled after the stream, so nothing here waits
-  // The allow-mask words of the slice are staged in LDS: one batched load
-  // overlapping the first stream round trip, then a barrier before any fold.
-  constexpr int kMaskPer = (kPenWords + kFT - 1) / kFT;
+  // ---- 0. counters, histograms and penalty bitmap cleared, first batch of
+  // history ids requested
+  const int lane = tid & (kWave - 1);
+  if (tid == 0) {
+    sm.chunk_ctr = 0u;
+    sm.pool_n = 0u;
+    sm.kmax16 = 0u;
+    sm.bucket = -1;
+    sm.parrive = 0u;
+    sm.theta_ready = 0u;
+  }
+  for (int i = tid; i < kPHist; i += kFT) sm.phist[i] = 0u;
+  if (fa.use_pen)
+    for (int i = tid; i < nw; i += kFT) sm.pen[i] = 0u;
+  __syncthreads();
+  // history ids past the first kHistPer x 1024 (long histories only): set
+  // their bits now, before the stream's loads are in flight
+  bool bad_hist = false;
+  auto hist_bits = [&](int32_t id) {
+    if (id >= a.V)
+      bad_hist = true;
+    else if (fa.use_pen && id >= e0 && id < e1)
+      atomicOr(&sm.pen[(uint32_t)(id >> 5) - c.w0], 1u << (id & 31));
+  };
+  if (read_hist)
+    for (int64_t j = (int64_t)kHistPer * kFT + tid; j < a.hist_len; j += kFT) hist_bits(hrow[j]);
+  // the first batch: requested now, used by the pilot
   int32_t hv[kHistPer];
-  auto setup = [&]() {
-    uint32_t mw[kMaskPer];
-    if (c.mrow) {
 #pragma unroll
-      for (int q = 0; q < kMaskPer; ++q) {
-        const int i = tid + q * kFT;
-        mw[q] = i < nw ? c.mrow[c.w0 + i] : 0u;
-      }
-    }
-    if (read_hist) {
+  for (int q = 0; q < kHistPer; ++q) {
+    const int64_t j = tid + (int64_t)q * kFT;
+    hv[q] = read_hist && j < a.hist_len ? hrow[j] : -1;
+  }
+
+  // ---- 1. stream with a prefix pilot.
+  // Every token of the slice is folded into the raw log-sum-exp (the logprob
+  // output).  The pilot -- the slice's first kNP x 1024 vectors, requested
+  // before the rest -- sets the capture threshold: theta1 is the Kc-th
+  // largest, over the 1024 threads, of the thread's largest allowed
+  // penalised pilot logit (rounded down to bf16).  Threads hold disjoint
+  // tokens, so at least Kc allowed tokens have a penalised logit >= theta1,
+  // and a token can only outrank them if its raw value reaches theta
+  // (theta1 mapped back through the penalty's largest increase and lowered
+  // by 2^-12).  Every allowed token with x >= theta is captured into the LDS
+  // pool (ckey holds the id, cx the raw logit); a lane whose block maximum
+  // is below theta only pays one compare.  Exactness is checked after the
+  // stream.
+  Lse3 st{kNegInf, 0.0f, 0.0f};
+  float theta = kNegInf;
+  auto allow_bits = [&](uint32_t sw, int64_t vi) -> uint32_t {
+    if constexpr (kMask)
+      return (sw >> ((uint32_t)(vi * E) & 31u)) & ((1u << E) - 1u);
+    else
+      return (1u << E) - 1u;
+  };
+  auto capture = [&](const float(&xv)[E], uint32_t sw, int64_t vi) {
+    uint32_t cand = 0;
 #pragma unroll
-      for (int q = 0; q < kHistPer; ++q) {
-        const int64_t j = tid + (int64_t)q * kFT;
-        hv[q] = j < a.hist_len ? hrow[j] : -1;
-      }
-    }
-    if (fa.use_pen)
-      for (int i = tid; i < nw; i += kFT) sm.pen[i] = 0u;
-    if (c.mrow) {
+    for (int j = 0; j < E; ++j) cand |= (xv[j] >= theta && xv[j] > kNegInf ? 1u : 0u) << j;
+    cand &= allow_bits(sw, vi);
+    while (cand) {
+      const int j = __builtin_ctz(cand);
+      cand &= cand - 1u;
+      float xj = xv[0];  // xv[j] without a dynamic register index
 #pragma unroll
-      for (int q = 0; q < kMaskPer; ++q) {
-        const int i = tid + q * kFT;
-        if (i < nw) sm.maskw[i] = mw[q];
+      for (int q = 1; q < E; ++q) xj = q == j ? xv[q] : xj;
+      const uint32_t slot = atomicAdd(&sm.pool_n, 1u);
+      if (slot < (uint32_t)kCand) {
+        sm.ckey[slot] = (unsigned long long)(uint32_t)(vi * E + j);
+        sm.cx[slot] = xj;
       }
-      __syncthreads();
     }
   };
-
-  // ---- 1. stream: raw log-sum-exp and per-vector keys
-  Lse3 st{kNegInf, 0.0f, 0.0f};
-  uint32_t nz = 0, allowed = 0;
-  float rmax = kNegInf;  // largest vector maximum (its key is the slice's largest)
-  auto fold = [&](float(&x)[kFG][E], const uint32_t(&)[kFG], int64_t vbase, bool last) {
+  // the thread's pilot key and the wave's arrival; the last wave to arrive
+  // turns the 1024 keys into the threshold (no block barrier: waves that
+  // arrive first go on issuing their own loads)
+  auto pre = [&](const u32x4(&pv)[kNP], const uint32_t(&psw)[kNP], int64_t np) {
+    float mx = kNegInf;  // the thread's largest allowed raw pilot logit
+#pragma unroll
+    for (int q = 0; q < kNP; ++q) {
+      const int64_t rel = (int64_t)q * kFT + tid;
+      if (rel < np) {
+        float x[1][E];
+        Vec<T>::cvt(pv[q], x[0]);
+        lse_fold_block_max<false, 1, E>(st, x, vec_max<E>(x[0]));
+        const uint32_t mb = allow_bits(psw[q], c.v0 + rel);
+#pragma unroll
+        for (int j = 0; j < E; ++j) mx = ((mb >> j) & 1u) ? max3raw(mx, x[0][j], x[0][j]) : mx;
+      }
+    }
+    // lower bound of its penalised value (the history bitmap is not needed)
+    const float lv = (fa.use_pen && a.rho >= 1.0f && mx > kNegInf)
+                         ? (mx < 0.0f ? mx * a.rho : mx / a.rho) : mx;
+    // the wave's 16 largest keys (0: no allowed token) to LDS
+    uint32_t k16[1] = {lv > kNegInf ? ord32(lv) >> 16 : 0u};
+    wave_sort_desc<1>(k16);
+    if (lane < kWTop) sm.wtop[(tid / kWave) * kWTop + lane] = k16[0];
+    uint32_t arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&sm.parrive, 1u);
+    if (__builtin_amdgcn_readfirstlane(arrived) != (uint32_t)kFWaves - 1u) return;
+    // last wave: theta1 = the Kc-th largest of the posted keys.  They are
+    // keys of distinct threads, so at least Kc threads reach it (exact
+    // unless one wave held more than 16 of the Kc largest).
+    uint32_t t16 = 0;
+    const uint32_t r = (Kc - 1u) / kWave, l = (Kc - 1u) % kWave;
+    if (Kc <= (uint32_t)kWave) {
+      uint32_t v[2];  // the 8 largest keys of each wave suffice
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int e = q * kWave + lane;
+        v[q] = sm.wtop[(e / 8) * kWTop + (e % 8)];
+      }
+      wave_sort_desc<2>(v);
+      t16 = (uint32_t)__shfl((int)v[0], (int)l, kWave);
+    } else {
+      uint32_t v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = sm.wtop[q * kWave + lane];
+      wave_sort_desc<4>(v);
+      const uint32_t vr = r == 0 ? v[0] : v[1];  // Kc <= 128
+      t16 = (uint32_t)__shfl((int)vr, (int)l, kWave);
+    }
+    float t1 = t16 ? unord32(t16 << 16) : kNegInf;
+    if (t1 > kNegInf) {
+      // smallest raw x whose penalised value can reach t1
+      if (fa.use_pen && a.rho < 1.0f) t1 = t1 > 0.0f ? t1 * a.rho : t1 / a.rho;
+      t1 = t1 - __builtin_fabsf(t1) * 0x1p-12f - 0x1p-100f;
+    }
+    if (lane == 0) {
+      sm.theta_bits = f2u(t1);
+      __hip_atomic_store(&sm.theta_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  // with the first chunks in flight: the first history batch into the
+  // penalty bitmap, then the threshold, then the pilot's own tokens
+  auto post = [&](const u32x4(&pv)[kNP], const uint32_t(&psw)[kNP], int64_t np) {
+#pragma unroll
+    for (int q = 0; q < kHistPer; ++q)
+      if (hv[q] >= 0) hist_bits(hv[q]);
+    while (__hip_atomic_load(&sm.theta_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
+      __builtin_amdgcn_s_sleep(1);
+    theta = u2f(__hip_atomic_load(&sm.theta_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+#pragma unroll
+    for (int q = 0; q < kNP; ++q) {
+      const int64_t rel = (int64_t)q * kFT + tid;
+      if (rel < np) {
+        float x[E];
+        Vec<T>::cvt(pv[q], x);
+        if (vec_max<E>(x) >= theta) capture(x, psw[q], c.v0 + rel);
+      }
+    }
+  };
+  auto fold = [&](float(&x)[kFG][E], const uint32_t(&sw)[kFG], int64_t vbase, bool last) {
     float gm[kFG];
 #pragma unroll
     for (int k = 0; k < kFG; ++k) gm[k] = vec_max<E>(x[k]);
@@ -705,183 +895,259 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     for (int k = 1; k + 1 < kFG; k += 2) cm = max3raw(cm, gm[k], gm[k + 1]);
     if (!(kFG & 1)) cm = max3raw(cm, gm[kFG - 1], gm[kFG - 1]);
     lse_fold_block_max<false, kFG, E>(st, x, cm);
+    if (cm >= theta) {
 #pragma unroll
-    for (int k = 0; k < kFG; ++k) {
-      const int64_t vi = vbase + (int64_t)k * kWave;
-      if (!last || vi < c.v1) {
-        uint32_t key = vec_key<T>(gm[k]);
-        if (c.mrow) {
-          const uint32_t mb = c.mask_bits(sm, vi * E, E);
-          if (mb == 0u) {
-            key = 0u;
-            gm[k] = kNegInf;
-          } else {
-            ++nz;
-            allowed += __builtin_popcount(mb);
-          }
-        }
-        sm.u.gkey[vi - c.v0] = (uint16_t)key;
-        rmax = max3raw(rmax, gm[k], gm[k]);
-      }
+      for (int k = 0; k < kFG; ++k)
+        if (gm[k] >= theta) capture(x[k], sw[k], vbase + (int64_t)k * kWave);
     }
   };
-  // non-temporal: the row is read once; the few vectors re-read during
-  // selection come back from the MALL
-  stream_vectors_dyn<T, kFG, true, false>(c.row, c.v0, c.v1, nullptr, 0, &sm.chunk_ctr, fold,
-                                         setup);
+  // non-temporal: the row is read once
+  stream_vectors_prefix<T, kFT, kNP, kFG, true, kMask>(
+      c.row, c.v0, c.v1, c.mrow, kMask ? (E == 8 ? 2 : 3) : 0, &sm.chunk_ctr, pre, post, fold);
+  // tokens past the last whole vector (last slice only)
   for (int64_t id = c.tail0 + tid; id < a.V; id += kFT) {
     float x[1][4] = {{Elem<T>::get(c.row, id), kNegInf, kNegInf, kNegInf}};
     lse_fold_block_max<false, 1, 4>(st, x, x[0][0]);
+    const float xv = x[0][0];
+    if (xv >= theta && xv > kNegInf && c.mask_bits(id, 1)) {
+      const uint32_t slot = atomicAdd(&sm.pool_n, 1u);
+      if (slot < (uint32_t)kCand) {
+        sm.ckey[slot] = (unsigned long long)(uint32_t)id;
+        sm.cx[slot] = xv;
+      }
+    }
   }
-  // keys past the slice inside its last 16-byte chunk read as 0
-  if (tid < 8 && c.nv + tid < ((c.nv + 7) & ~7)) sm.u.gkey[c.nv + tid] = 0;
+  bad_hist = __syncthreads_or(bad_hist);  // also completes the pool and the bitmap
+  float lm = st.m, ls = st.s;
+  block_lse2<kFT>(lm, ls, sm.red);
 
-  // one combined block reduction: (m, s), the largest vector maximum, nz,
-  // allowed.  Its barrier also orders the bitmap clearing before the history
-  // atomics below.
-  Lse3 lse;
-  uint32_t kmax;
-  {
+  // ---- 2. resolve the pool: exact processed logits and order keys.  Every
+  // token left out has x < theta, so its processed logit is <= yex; the pool
+  // holds the slice's top Kc when at least Kc pooled tokens beat yex (or when
+  // theta is -inf and every allowed token was pooled).  Of those, a 16-bit
+  // key histogram keeps the ones at or above the Kc-th key for ranking.
+  const uint32_t pool_n = sm.pool_n;
+  const uint32_t npool = pool_n < (uint32_t)kCand ? pool_n : (uint32_t)kCand;
+  const float yex = theta > kNegInf ? c.proc.ub(theta) : kNegInf;
+  constexpr int kPer = kCand / kFT;
+  unsigned long long pk[kPer];
+  float px[kPer];
+  uint32_t pk16[kPer];
+  uint32_t nval = 0, mx16 = 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const Lse3 w{__shfl_xor(st.m, o, kWave), __shfl_xor(st.s, o, kWave), 0.0f};
-      st = lse3_merge(st, w);
-      rmax = fmaxf(rmax, __shfl_xor(rmax, o, kWave));
-      nz += __shfl_xor(nz, o, kWave);
-      allowed += __shfl_xor(allowed, o, kWave);
-    }
-    const int lane = tid & (kWave - 1), wid = tid / kWave;
-    if (lane == 0) {
-      sm.redx[wid][0] = f2u(st.m);
-      sm.redx[wid][1] = f2u(st.s);
-      sm.redx[wid][2] = f2u(rmax);
-      sm.redx[wid][3] = nz;
-      sm.redx[wid][4] = allowed;
-    }
-    __syncthreads();
-    lse = Lse3{kNegInf, 0.0f, 0.0f};
-    rmax = kNegInf;
-    nz = 0;
-    allowed = 0;
-    for (int w = 0; w < kFWaves; ++w) {
-      lse = lse3_merge(lse, Lse3{u2f(sm.redx[w][0]), u2f(sm.redx[w][1]), 0.0f});
-      rmax = fmaxf(rmax, u2f(sm.redx[w][2]));
-      nz += sm.redx[w][3];
-      allowed += sm.redx[w][4];
-    }
-    kmax = rmax > kNegInf ? vec_key<T>(rmax) : 0u;
-    if (!c.mrow) {
-      nz = (uint32_t)c.nv;
-      allowed = (uint32_t)c.nv * E;
-    }
-  }
-  // penalty bitmap of the slice from the history ids
-  bool bad_hist = false;
-  if (read_hist) {
-    for (int64_t j0 = 0; j0 < a.hist_len; j0 += (int64_t)kHistPer * kFT) {
-      if (j0 > 0) {
-        for (int q = 0; q < kHistPer; ++q) {
-          const int64_t j = j0 + tid + (int64_t)q * kFT;
-          hv[q] = j < a.hist_len ? hrow[j] : -1;
-        }
-      }
-      for (int q = 0; q < kHistPer; ++q) {
-        const int32_t id = hv[q];
-        if (id >= a.V) {
-          bad_hist = true;
-        } else if (fa.use_pen && id >= e0 && id < e1) {
-          atomicOr(&sm.pen[(uint32_t)(id >> 5) - c.w0], 1u << (id & 31));
-        }
+  for (int q = 0; q < kPer; ++q) {
+    const uint32_t i = (uint32_t)tid + (uint32_t)q * kFT;
+    pk[q] = 0ull;
+    px[q] = 0.0f;
+    pk16[q] = 0u;
+    if (i < npool) {
+      const int32_t id = (int32_t)(uint32_t)sm.ckey[i];
+      const float x = sm.cx[i];
+      const bool pen = fa.use_pen && ((sm.pen[(uint32_t)(id >> 5) - c.w0] >> (id & 31)) & 1u);
+      const float y = c.proc.y(x, pen);
+      if (y > yex) {
+        pk[q] = rank_key(y, id);
+        px[q] = x;
+        pk16[q] = ord32(y) >> 16;
+        ++nval;
+        mx16 = max(mx16, pk16[q]);
       }
     }
   }
-  bad_hist = __syncthreads_or(bad_hist);
-
-  // ---- 2. select the slice's top Kc
-  const uint32_t Kc = (uint32_t)fa.Kc;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    nval += (uint32_t)__shfl_xor((int)nval, o, kWave);
+    mx16 = max(mx16, (uint32_t)__shfl_xor((int)mx16, o, kWave));
+  }
+  if (lane == 0) {
+    sm.redu[tid / kWave] = nval;
+    if (mx16) atomicMax(&sm.kmax16, mx16);
+  }
+  __syncthreads();
+  uint32_t nbeat = 0;
+#pragma unroll
+  for (int w = 0; w < kFWaves; ++w) nbeat += sm.redu[w];
+  const bool pool_exact = pool_n <= (uint32_t)kCand && (theta == kNegInf || nbeat >= Kc);
   uint32_t tau = 1u;
   float xout = kNegInf, yout = kNegInf;
   uint32_t ngt = 0;
-  const bool has_tail = c.tail0 < a.V;
-  if (kmax > 0u || has_tail) {
-    // allowed tokens per vector among vectors with one: roughly the chance
-    // that a re-read vector contributes a token above the threshold
-    const float dens = nz ? (float)allowed / (float)(nz * E) : 1.0f;
-    uint32_t need = (uint32_t)__builtin_ceilf(2.0f * (float)Kc / dens) + 32u;
-    // large slices histogram a 1-in-8 sample of the keys (the threshold only
-    // steers how many vectors are re-read; exactness is checked below)
-    const bool sampled = c.nv > 8192;
-    const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.gkey);
-    const int nchunk = (c.nv + 7) >> 3;
-    int shift = 0;
-    for (int attempt = 0; attempt < 4; ++attempt) {
-      if (attempt < 3 && kmax > 1u) {
-        __syncthreads();
-        if (tid < 256) sm.hist[tid] = 0u;
-        if (tid == 0) {
-          sm.bucket = 0;  // fewer than `need` keys in range: take the whole range
-          sm.above = 0;
+  int nthr = kFT;  // threads that take part from here on
+  if (pool_exact) {
+    // keys at or above the Kc-th key (16-bit), found by wave 0
+    uint32_t t16 = 0;
+    if (nbeat > 256u) {
+      const uint32_t km = sm.kmax16;
+#pragma unroll
+      for (int q = 0; q < kPer; ++q)
+        if (pk[q] && km - pk16[q] < (uint32_t)kPHist) atomicAdd(&sm.phist[kPHist - 1 - (km - pk16[q])], 1u);
+      __syncthreads();
+      if (tid < kWave) {
+        const int32_t bk = wave_find_bucket<kPHist>(sm.phist, Kc - 1u);
+        if (tid == 0) sm.bucket = bk;
+      }
+      __syncthreads();
+      if (sm.bucket >= 0) t16 = km - (uint32_t)(kPHist - 1 - sm.bucket);
+    }
+    // compaction into ckey / cx (every thread has read its pool entries
+    // before the barrier above): one slot reservation per wave
+    if (tid == 0) sm.ngt = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const bool keep = pk[q] && pk16[q] >= t16;
+      const unsigned long long m = __ballot(keep);
+      uint32_t base = 0;
+      if (lane == 0 && m) base = atomicAdd(&sm.ngt, (uint32_t)__builtin_popcountll(m));
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (keep) {
+        const uint32_t slot = base + (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
+        sm.ckey[slot] = pk[q];
+        sm.cx[slot] = px[q];
+      }
+    }
+    __syncthreads();
+    ngt = sm.ngt;
+    // a whole row in this workgroup: ranking and finish use one wave per
+    // SIMD; the other waves only pass the barriers
+    if (S == 1) nthr = kTT;
+  } else {
+    // ---- 2b. fallback (pool overflow or no separation, e.g. massive exact
+    // ties): per-vector keys of the slice re-read from HBM, then the
+    // threshold search below.
+    uint32_t nz = 0, allowed = 0;
+    float rmax = kNegInf;
+    const u32x4* rv = reinterpret_cast<const u32x4*>(c.row);
+    for (int64_t vi = c.v0 + tid; vi < c.v1; vi += kFT) {
+      float xv[E];
+      Vec<T>::cvt(rv[vi], xv);
+      float g = vec_max<E>(xv);
+      uint32_t key = vec_key<T>(g);
+      if (kMask) {
+        const uint32_t mb = c.mask_bits(vi * E, E);
+        if (mb == 0u) {
+          key = 0u;
+          g = kNegInf;
+        } else {
+          ++nz;
+          allowed += __builtin_popcount(mb);
         }
-        __syncthreads();
-        for (int j = tid; j < nchunk; j += kFT) {
-          const u32x4 w = keys[j];
-          const uint32_t kk[4] = {w.x, w.y, w.z, w.w};
-          for (int e = 0; e < (sampled ? 1 : 8); ++e) {
-            const uint32_t k = (e & 1) ? (kk[e >> 1] >> 16) : (kk[e >> 1] & 0xFFFFu);
-            if (k >= 1u) {
-              const uint32_t d = (kmax - k) >> shift;
-              if (d < 256u) atomicAdd(&sm.hist[255 - d], 1u);
+      }
+      sm.u.gkey[vi - c.v0] = (uint16_t)key;
+      rmax = max3raw(rmax, g, g);
+    }
+    // keys past the slice inside its last 16-byte chunk read as 0
+    if (tid < 8 && c.nv + tid < ((c.nv + 7) & ~7)) sm.u.gkey[c.nv + tid] = 0;
+    uint32_t kmax;
+    {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        rmax = fmaxf(rmax, __shfl_xor(rmax, o, kWave));
+        nz += __shfl_xor(nz, o, kWave);
+        allowed += __shfl_xor(allowed, o, kWave);
+      }
+      const int lane = tid & (kWave - 1), wid = tid / kWave;
+      __syncthreads();
+      if (lane == 0) {
+        sm.redx[wid][2] = f2u(rmax);
+        sm.redx[wid][3] = nz;
+        sm.redx[wid][4] = allowed;
+      }
+      __syncthreads();
+      rmax = kNegInf;
+      nz = 0;
+      allowed = 0;
+      for (int w = 0; w < kFWaves; ++w) {
+        rmax = fmaxf(rmax, u2f(sm.redx[w][2]));
+        nz += sm.redx[w][3];
+        allowed += sm.redx[w][4];
+      }
+      kmax = rmax > kNegInf ? vec_key<T>(rmax) : 0u;
+      if (!kMask) {
+        nz = (uint32_t)c.nv;
+        allowed = (uint32_t)c.nv * E;
+      }
+    }
+    const bool has_tail = c.tail0 < a.V;
+    if (kmax > 0u || has_tail) {
+      // allowed tokens per vector among vectors with one: roughly the chance
+      // that a re-read vector contributes a token above the threshold
+      const float dens = nz ? (float)allowed / (float)(nz * E) : 1.0f;
+      uint32_t need = (uint32_t)__builtin_ceilf(2.0f * (float)Kc / dens) + 32u;
+      // large slices histogram a 1-in-8 sample of the keys (the threshold only
+      // steers how many vectors are re-read; exactness is checked below)
+      const bool sampled = c.nv > 8192;
+      const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.gkey);
+      const int nchunk = (c.nv + 7) >> 3;
+      int shift = 0;
+      for (int attempt = 0; attempt < 4; ++attempt) {
+        if (attempt < 3 && kmax > 1u) {
+          __syncthreads();
+          if (tid < 256) sm.hist[tid] = 0u;
+          if (tid == 0) {
+            sm.bucket = 0;  // fewer than `need` keys in range: take the whole range
+            sm.above = 0;
+          }
+          __syncthreads();
+          for (int j = tid; j < nchunk; j += kFT) {
+            const u32x4 w = keys[j];
+            const uint32_t kk[4] = {w.x, w.y, w.z, w.w};
+            for (int e = 0; e < (sampled ? 1 : 8); ++e) {
+              const uint32_t k = (e & 1) ? (kk[e >> 1] >> 16) : (kk[e >> 1] & 0xFFFFu);
+              if (k >= 1u) {
+                const uint32_t d = (kmax - k) >> shift;
+                if (d < 256u) atomicAdd(&sm.hist[255 - d], 1u);
+              }
             }
           }
+          __syncthreads();
+          // bucket (from the top) where the count of passing vectors reaches need
+          const uint32_t need_h = sampled ? (need + 7u) / 8u : need;
+          find_bucket(sm, need_h - 1u);
+          __syncthreads();
+          const uint32_t bt = 255u - (uint32_t)sm.bucket;  // distance bin from kmax
+          const int64_t lo = (int64_t)kmax - (int64_t)((bt + 1u) << shift) + 1;
+          tau = lo > 1 ? (uint32_t)lo : 1u;
+        } else {
+          tau = 1u;
         }
+        xout = tau > 1u ? key_value(tau - 1u) : kNegInf;
+        yout = tau > 1u ? c.proc.ub(xout) : kNegInf;
+        if (tid == 0) sm.ngt = 0u;
         __syncthreads();
-        // bucket (from the top) where the count of passing vectors reaches need
-        const uint32_t need_h = sampled ? (need + 7u) / 8u : need;
-        find_bucket(sm, need_h - 1u);
-        __syncthreads();
-        const uint32_t bt = 255u - (uint32_t)sm.bucket;  // distance bin from kmax
-        const int64_t lo = (int64_t)kmax - (int64_t)((bt + 1u) << shift) + 1;
-        tau = lo > 1 ? (uint32_t)lo : 1u;
-      } else {
-        tau = 1u;
-      }
-      xout = tau > 1u ? key_value(tau - 1u) : kNegInf;
-      yout = tau > 1u ? c.proc.ub(xout) : kNegInf;
-      if (tid == 0) sm.ngt = 0u;
-      __syncthreads();
-      uint32_t nsel = 0;
-      auto collect = [&](int32_t id, float y, float x) {
-        const uint32_t slot = atomicAdd(&sm.ngt, 1u);
-        if (slot < (uint32_t)kCand) {
-          sm.ckey[slot] = rank_key(y, id);
-          sm.cx[slot] = x;
-        }
-      };
-      {
-        const uint32_t total = select_vectors(sm, c.nv, tau, 0);
-        nsel = total;
-        for (uint32_t base = 0; base < total; base += kSel) {
-          if (base > 0) select_vectors(sm, c.nv, tau, base);
-          const uint32_t n = total - base < (uint32_t)kSel ? total - base : (uint32_t)kSel;
-          emit_listed<T>(sm, c, n, xout, yout, collect);
+        uint32_t nsel = 0;
+        auto collect = [&](int32_t id, float y, float x) {
+          const uint32_t slot = atomicAdd(&sm.ngt, 1u);
+          if (slot < (uint32_t)kCand) {
+            sm.ckey[slot] = rank_key(y, id);
+            sm.cx[slot] = x;
+          }
+        };
+        {
+          const uint32_t total = select_vectors(sm, c.nv, tau, 0);
+          nsel = total;
+          for (uint32_t base = 0; base < total; base += kSel) {
+            if (base > 0) select_vectors(sm, c.nv, tau, base);
+            const uint32_t n = total - base < (uint32_t)kSel ? total - base : (uint32_t)kSel;
+            emit_listed<T>(sm, c, n, xout, yout, collect);
+            __syncthreads();
+          }
+          emit_tail<T>(sm, c, xout, yout, collect);
           __syncthreads();
         }
-        emit_tail<T>(sm, c, xout, yout, collect);
-        __syncthreads();
+        ngt = sm.ngt;
+        if (tau <= 1u || (ngt >= Kc && ngt <= (uint32_t)kCand)) break;
+        // move the threshold by the measured rate of kept tokens per vector
+        if (ngt > (uint32_t)kCand) {
+          const uint64_t t = (uint64_t)nsel * (uint64_t)(kCand / 2) / ngt;
+          need = t > Kc ? (uint32_t)t : Kc;
+        } else if (ngt > 0u) {
+          const uint64_t t = (uint64_t)nsel * 2u * Kc / ngt + 32u;
+          need = t < 0x7FFFFFFFull ? (uint32_t)t : 0x7FFFFFFFu;
+        } else {
+          need = need < 0x0FFFFFFFu ? need * 8u + 64u : 0x7FFFFFFFu;
+        }
+        shift = need > 4096u ? 3 : (need > 1024u ? 1 : 0);
       }
-      ngt = sm.ngt;
-      if (tau <= 1u || (ngt >= Kc && ngt <= (uint32_t)kCand)) break;
-      // move the threshold by the measured rate of kept tokens per vector
-      if (ngt > (uint32_t)kCand) {
-        const uint64_t t = (uint64_t)nsel * (uint64_t)(kCand / 2) / ngt;
-        need = t > Kc ? (uint32_t)t : Kc;
-      } else if (ngt > 0u) {
-        const uint64_t t = (uint64_t)nsel * 2u * Kc / ngt + 32u;
-        need = t < 0x7FFFFFFFull ? (uint32_t)t : 0x7FFFFFFFu;
-      } else {
-        need = need < 0x0FFFFFFFu ? need * 8u + 64u : 0x7FFFFFFFu;
-      }
-      shift = need > 4096u ? 3 : (need > 1024u ? 1 : 0);
     }
   }
 
@@ -904,17 +1170,17 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   if (ngt <= 256u) {
     rank_sort_small(sm.ckey, sm.cx, ngt, Kc, put);
   } else {
-    select_top_slow<T>(sm, c, ngt, Kc, tau, xout, yout);
+    select_top_slow<T>(sm, c, ngt, Kc, tau, xout, yout, nthr);
     rank_sort_small(sm.skey, sm.sx, Kc, Kc, put);
   }
   __syncthreads();
   if (S == 1) {
-    finish_row(sm, fa, b, lse, bad_hist, nout);
+    finish_row(sm, fa, b, lm, ls, bad_hist, nout);
     return;
   }
   if (tid == 0) {
-    head->m = lse.m;
-    head->s = lse.s;
+    head->m = lm;
+    head->s = ls;
     head->n = nout;
     head->flags = (s == 0 && bad_hist) ? 1u : 0u;
   }
@@ -928,19 +1194,14 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   if (tid == 0) {
     __threadfence();
     uint32_t* cnt = reinterpret_cast<uint32_t*>(fa.ws) + b;
-    uint32_t old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t arrived;
-    while (true) {
-      const uint32_t nw2 = (old >> 16) == fa.epoch ? old + 1u : (fa.epoch << 16) | 1u;
-      const uint32_t prev = atomicCAS(cnt, old, nw2);
-      if (prev == old) {
-        arrived = nw2 & 0xFFFFu;
-        break;
-      }
-      old = prev;
-    }
+    const uint32_t arrived = atomicAdd(cnt, 1u) + 1u;
     const bool last = arrived == (uint32_t)S;
-    if (last) __threadfence();
+    if (last) {
+      // Every workgroup of the row has arrived, so nothing else touches the
+      // counter in this launch: return it to zero for the next call.
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence();
+    }
     sm.flag = last ? 1 : 0;
   }
   __syncthreads();
@@ -984,7 +1245,7 @@ FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p,
   const int64_t nvec = V / E;
   if (!aligned || Kc < 1 || Kc > kFastK || nvec < 64 || B < 1 || B > 0xFFFF) return pl;
   const int64_t s_min = (nvec + kSliceVecs - 1) / kSliceVecs;
-  const int64_t s_cap = kCand / Kc < kMaxSlices ? kCand / Kc : kMaxSlices;
+  const int64_t s_cap = kMergeCand / Kc < kMaxSlices ? kMergeCand / Kc : kMaxSlices;
   if (s_min > s_cap) return pl;
   const int64_t cus = device_cus();
   int64_t S = (cus + B - 1) / B;
@@ -1004,8 +1265,6 @@ FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p,
   }
   return pl;
 }
-
-std::atomic<uint32_t> g_epoch{0};
 
 }  // namespace gtp
 
@@ -1076,22 +1335,25 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
   fa.vps = pl.vps;
   fa.ws = reinterpret_cast<unsigned char*>(workspace);
   fa.cnt_bytes = pl.cnt_bytes;
-  fa.epoch = (g_epoch.fetch_add(1u, std::memory_order_relaxed) % 0xFFFFu) + 1u;
   fa.greedy = greedy ? 1 : 0;
   fa.Kc = greedy ? 1 : params->top_k;
   fa.use_pen = (history && hist_len > 0 && params->repetition_penalty != 1.0f) ? 1 : 0;
   fa.p_active = (!greedy && params->top_p > 0.0f && params->top_p < 1.0f) ? 1 : 0;
   fa.Tc = params->temperature > 1e-6f ? params->temperature : 1e-6f;
   const dim3 grid((unsigned)pl.S, (unsigned)B), block(kFT);
+  const bool m = allow_mask != nullptr;
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      hipLaunchKernelGGL(sampler_split_kernel<uint16_t>, grid, block, 0, st, fa);
+      if (m) hipLaunchKernelGGL((sampler_split_kernel<uint16_t, true>), grid, block, 0, st, fa);
+      else hipLaunchKernelGGL((sampler_split_kernel<uint16_t, false>), grid, block, 0, st, fa);
       break;
     case GTP_DTYPE_F16:
-      hipLaunchKernelGGL(sampler_split_kernel<_Float16>, grid, block, 0, st, fa);
+      if (m) hipLaunchKernelGGL((sampler_split_kernel<_Float16, true>), grid, block, 0, st, fa);
+      else hipLaunchKernelGGL((sampler_split_kernel<_Float16, false>), grid, block, 0, st, fa);
       break;
     default:
-      hipLaunchKernelGGL(sampler_split_kernel<float>, grid, block, 0, st, fa);
+      if (m) hipLaunchKernelGGL((sampler_split_kernel<float, true>), grid, block, 0, st, fa);
+      else hipLaunchKernelGGL((sampler_split_kernel<float, false>), grid, block, 0, st, fa);
       break;
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;

@@ -178,6 +178,36 @@ __device__ __forceinline__ Lse3 block_lse3(Lse3 v, float (*red)[3]) {
   return r;
 }
 
+// (m, s) merge over a wave without per-step exponentials: the wave maximum
+// first, then one rescale per lane and a plain sum.  NaN in s (a NaN or +inf
+// logit) stays NaN.
+__device__ __forceinline__ void wave_lse2(float& m, float& s) {
+  float mw = m;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o, kWave));
+  float sv = m == mw ? s : s * __builtin_amdgcn_exp2f((m - mw) * kLog2e);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sv += __shfl_xor(sv, o, kWave);
+  m = mw;
+  s = sv;
+}
+
+// Block-wide (m, s) of NT threads; every thread gets the result.  `red`
+// holds 2 floats per wave; callers sync before reusing it.
+template <int NT>
+__device__ __forceinline__ void block_lse2(float& m, float& s, float (*red)[3]) {
+  wave_lse2(m, s);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (lane == 0) {
+    red[wid][0] = m;
+    red[wid][1] = s;
+  }
+  __syncthreads();
+  m = lane < NT / kWave ? red[lane][0] : kNegInf;
+  s = lane < NT / kWave ? red[lane][1] : 0.0f;
+  wave_lse2(m, s);
+}
+
 struct NoPrologue {
   __device__ __forceinline__ void operator()() const {}
 };
@@ -336,6 +366,94 @@ __device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, in
     ca = grab();
     issue(a, sa, ca);
     consume(b, sb, cb);
+  }
+}
+
+// Stream vectors [v0, v1) (v1 > v0) of a 16-byte aligned row with a prefix
+// pilot.  Thread t loads the pilot vectors v0 + q*NT + t (q < NP, inside the
+// range; np = number of pilot vectors, entries at or past np re-read the
+// first vector) and calls `pre(p, sp, np)` on them before any other load is
+// issued; then the wave's first two chunks of the rest are issued and
+// `post(p, sp, np)` runs with them in flight.  `pre` must not hold block
+// barriers: a wave that waits on another before issuing its own loads lets
+// the memory pipeline drain.  The rest of the range is streamed as in
+// stream_vectors_dyn: `fold(x, sw, vec_index, last)`, vector k of the block
+// at vec_index + k*64.
+template <typename T, int NT, int NP, int NG, bool kNonTemporal, bool kSide, typename Pre,
+          typename Post, typename Fold>
+__device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row, int64_t v0,
+                                                      int64_t v1, const uint32_t* __restrict__ side,
+                                                      int side_shift, uint32_t* counter, Pre&& pre,
+                                                      Post&& post, Fold&& fold) {
+  constexpr int E = Vec<T>::kE;
+  constexpr uint32_t kChunk = (uint32_t)kWave * NG;
+  const int64_t n = v1 - v0 > 0 ? v1 - v0 : 0;
+  const int64_t np = n < (int64_t)NP * NT ? n : (int64_t)NP * NT;
+  const char* __restrict__ base = reinterpret_cast<const char*>(row) + v0 * 16;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (kWave - 1);
+  u32x4 p[NP];
+  uint32_t sp[NP];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    uint32_t vi = (uint32_t)q * NT + tid;
+    vi = vi < (uint32_t)np ? vi : 0u;
+    const u32x4* a = reinterpret_cast<const u32x4*>(base + vi * 16u);
+    p[q] = kNonTemporal ? __builtin_nontemporal_load(a) : *a;
+    sp[q] = kSide ? side[(uint64_t)(v0 + vi) >> side_shift] : 0xFFFFFFFFu;
+  }
+  pre(p, sp, np);
+  // the rest: [v0 + np, v1) in per-wave chunks (an empty rest re-reads the
+  // first vector of the range)
+  const int64_t off = np < n ? np : 0;
+  const char* __restrict__ base2 = base + off * 16;
+  const int64_t n2 = n - np;
+  const uint32_t nchunks = (uint32_t)((n2 + kChunk - 1) / kChunk);
+  const uint32_t last = n2 > 0 ? (uint32_t)(n2 - 1) : 0u;
+  auto grab = [&]() -> uint32_t {
+    uint32_t c = 0;
+    if (lane == 0) c = atomicAdd(counter, 1u);
+    return __builtin_amdgcn_readfirstlane(c);
+  };
+  u32x4 a[NG], b[NG];
+  uint32_t sa[NG], sb[NG];
+  auto issue = [&](u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t chunk) {
+    const bool live = chunk < nchunks;
+    const uint32_t first = chunk * kChunk + lane;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      uint32_t vi = first + (uint32_t)k * kWave;
+      vi = vi < last ? vi : last;
+      vi = live ? vi : 0u;
+      const u32x4* q = reinterpret_cast<const u32x4*>(base2 + vi * 16u);
+      if (kNonTemporal)
+        buf[k] = __builtin_nontemporal_load(q);
+      else
+        buf[k] = *q;
+      sbuf[k] = kSide ? side[(uint64_t)(v0 + off + vi) >> side_shift] : 0xFFFFFFFFu;
+    }
+  };
+  auto consume = [&](const u32x4(&buf)[NG], const uint32_t(&sbuf)[NG], uint32_t chunk) {
+    float x[NG][E];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
+    fold(x, sbuf, v0 + np + (int64_t)(chunk * kChunk + lane), chunk == nchunks - 1);
+  };
+  uint32_t ca = grab();
+  issue(a, sa, ca);
+  uint32_t cb = grab();
+  issue(b, sb, cb);
+  post(p, sp, np);
+  if (ca >= nchunks) return;
+  consume(a, sa, ca);
+  while (cb < nchunks) {
+    ca = grab();
+    issue(a, sa, ca);
+    consume(b, sb, cb);
+    if (ca >= nchunks) break;
+    cb = grab();
+    issue(b, sb, cb);
+    consume(a, sa, ca);
   }
 }
 
