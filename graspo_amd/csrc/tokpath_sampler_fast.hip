@@ -15,13 +15,16 @@
 //    a wave issues its first stream chunks as soon as it has posted, and
 //    only waits for theta with those loads in flight.
 // 2. Stream (the only HBM read of the slice; tokpath_stream.h).  Waves take
-//    chunks of 64 x 4 vectors from an LDS counter (the allow-mask word of
-//    each vector travels with it) and fold them into an online log-sum-exp
-//    of the raw logits (the logprob output).  Every allowed token with
-//    x >= theta (theta1 mapped back through the penalty's largest increase
-//    and lowered by 2^-12) is captured into an LDS pool of (id, x); a lane
-//    whose block maximum is below theta pays one compare.  History ids set
-//    a penalty bitmap in LDS while the first chunks are in flight.
+//    chunks of 64 x 4 vectors from an LDS counter (each lane also brings one
+//    allow-mask word of the chunk; slices start on word boundaries) and fold
+//    them into an online log-sum-exp of the raw logits (the logprob output).
+//    A vector whose maximum reaches theta (theta1 mapped back through the
+//    penalty's largest increase and lowered by 2^-12) is queued -- raw, with
+//    its slice index and allow bits -- in its wave's LDS queue, which is
+//    drained 64 vectors at a time, one per lane: the allowed tokens with
+//    x >= theta enter an LDS pool of (id, x).  A vector below theta costs one
+//    compare.  History ids set a penalty bitmap in LDS while the first
+//    chunks are in flight.
 // 3. Resolve.  The pooled tokens get the exact penalty, mask and IEEE
 //    division by the temperature.  A token left out has x < theta, so its
 //    processed logit is <= ub(theta); when at least Kc pooled tokens beat
@@ -60,6 +63,7 @@ constexpr int kCand = 2048;                 // candidate slots of a slice (the c
 constexpr int kMergeCand = 1024;            // entries of all slice lists of a row
 constexpr int kPHist = 1024;                // bins of the final 16-bit key filter
 constexpr int kWTop = 16;                   // pilot keys each wave posts (its largest)
+constexpr int kQCap = 128;                  // queued vectors per wave (drained at 64)
 // pilot vectors per thread (fp16 converts in more registers)
 template <typename T>
 constexpr int kNPof = Elem<T>::kDtype == GTP_DTYPE_F16 ? 3 : 4;
@@ -94,13 +98,19 @@ struct FastArgs {
 
 struct FastSmem {
   union {
-    uint16_t gkey[kSliceVecs];       // per-vector order keys of the slice
-    uint32_t soff[kMaxSlices + 1];   // merge: start of each slice's list in ckey / cx
+    struct {                          // during the stream
+      u32x4 qv[kFWaves][kQCap];       // each wave's queue of vectors whose maximum reached theta
+      uint32_t qi[kFWaves][kQCap];    // ... and their indices in the slice
+    } st;
+    struct {                          // fallback after the stream
+      uint16_t gkey[kSliceVecs];      // per-vector order keys of the slice
+      uint16_t sel[kSel];
+    } fb;
+    uint32_t soff[kMaxSlices + 1];    // merge: start of each slice's list in ckey / cx
   } u;
   uint32_t pen[kPenWords];           // penalty bitmap of the slice's tokens
   unsigned long long ckey[kCand];    // capture pool / candidates (slice), lists (merge)
   float cx[kCand];
-  uint16_t sel[kSel];
   unsigned long long skey[kFastK];   // the slice's survivors before sorting
   float sx[kFastK];
   unsigned long long fkey[kFastK];   // the row's top-k, sorted
@@ -117,7 +127,7 @@ struct FastSmem {
   uint32_t kmax16;     // block maximum of 16-bit order keys (pilot, final filter)
   uint32_t parrive;    // waves that have posted their pilot keys
   uint32_t theta_ready;
-  uint32_t theta_bits; // the capture threshold, once theta_ready
+  uint32_t theta_ord;  // ord32 of the capture threshold, once theta_ready
   uint32_t chunk_ctr;  // next stream chunk (per-wave dynamic schedule)
   int32_t bucket;
   uint32_t above;
@@ -369,7 +379,7 @@ __device__ __forceinline__ float vec_elem(const u32x4& v, int j) {
 // Returns the length of the whole list.  Block-uniform.
 __device__ __forceinline__ uint32_t select_vectors(FastSmem& sm, int nv, uint32_t tau,
                                                    uint32_t base) {
-  const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.gkey);
+  const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.fb.gkey);
   const int nchunk = (nv + 7) >> 3;
   uint32_t mine = 0;
   for (int j = threadIdx.x; j < nchunk; j += kFT) {
@@ -388,7 +398,7 @@ __device__ __forceinline__ uint32_t select_vectors(FastSmem& sm, int nv, uint32_
     for (int e = 0; e < 8; ++e) {
       const uint32_t key = (e & 1) ? (k[e >> 1] >> 16) : (k[e >> 1] & 0xFFFFu);
       if (key >= tau) {
-        if (pos >= base && pos < base + kSel) sm.sel[pos - base] = (uint16_t)(j * 8 + e);
+        if (pos >= base && pos < base + kSel) sm.u.fb.sel[pos - base] = (uint16_t)(j * 8 + e);
         ++pos;
       }
     }
@@ -398,7 +408,7 @@ __device__ __forceinline__ uint32_t select_vectors(FastSmem& sm, int nv, uint32_
 }
 
 // f(id, y, x) for every valid token with y > yout of the listed vectors
-// sm.sel[0, n).  yout = ub(xout), so a raw x <= xout never passes: only the
+// sm.u.fb.sel[0, n).  yout = ub(xout), so a raw x <= xout never passes: only the
 // few tokens above xout pay for the exact penalty and IEEE division.
 template <typename T, typename F>
 __device__ __forceinline__ void emit_listed(const FastSmem& sm, const Slice<T>& c, uint32_t n,
@@ -406,7 +416,7 @@ __device__ __forceinline__ void emit_listed(const FastSmem& sm, const Slice<T>& 
   constexpr int E = Vec<T>::kE;
   const u32x4* rv = reinterpret_cast<const u32x4*>(c.row);
   for (uint32_t p = threadIdx.x; p < n; p += kFT) {
-    const int64_t vi = c.v0 + sm.sel[p];
+    const int64_t vi = c.v0 + sm.u.fb.sel[p];
     const u32x4 v = rv[vi];
     const int64_t e0 = vi * E;
     const uint32_t mb = c.mask_bits(e0, E);
@@ -780,7 +790,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     else
       return (1u << E) - 1u;
   };
-  auto capture = [&](const float(&xv)[E], uint32_t sw, int64_t vi) {
+  auto capture = [&](const float(&xv)[E], uint32_t sw, int64_t vi) __attribute__((always_inline)) {
     uint32_t cand = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) cand |= (xv[j] >= theta && xv[j] > kNegInf ? 1u : 0u) << j;
@@ -797,6 +807,27 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
         sm.cx[slot] = xj;
       }
     }
+  };
+  // lower bound of the penalised value of raw x (the history is not consulted)
+  auto lb_pen = [&](float x) __attribute__((always_inline)) -> float {
+    return (fa.use_pen && a.rho >= 1.0f) ? (x < 0.0f ? x * a.rho : x / a.rho) : x;
+  };
+  // raw capture threshold for a 16-bit key t16 that at least Kc allowed
+  // penalised logits reach: the smallest raw x whose penalised value can reach
+  // it, lowered by 2^-12 (so that after the division by T every left-out token
+  // stays strictly below those Kc)
+  auto raw_of = [&](uint32_t t16) __attribute__((always_inline)) -> float {
+    if (!t16) return kNegInf;
+    float t1 = unord32(t16 << 16);
+    if (fa.use_pen && a.rho < 1.0f) t1 = t1 > 0.0f ? t1 * a.rho : t1 / a.rho;
+    return t1 - __builtin_fabsf(t1) * 0x1p-12f - 0x1p-100f;
+  };
+  // the Kc-th largest of 64 * R keys held by the wave (v: R per lane)
+  auto kth_key = [&](auto& v) __attribute__((always_inline)) -> uint32_t {
+    wave_sort_desc(v);
+    const uint32_t r = (Kc - 1u) / kWave, l = (Kc - 1u) % kWave;
+    const uint32_t vr = r == 0 ? v[0] : v[1];  // Kc <= 128 <= 64 R
+    return (uint32_t)__shfl((int)vr, (int)l, kWave);
   };
   // the thread's pilot key and the wave's arrival; the last wave to arrive
   // turns the 1024 keys into the threshold (no block barrier: waves that
@@ -816,8 +847,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       }
     }
     // lower bound of its penalised value (the history bitmap is not needed)
-    const float lv = (fa.use_pen && a.rho >= 1.0f && mx > kNegInf)
-                         ? (mx < 0.0f ? mx * a.rho : mx / a.rho) : mx;
+    const float lv = mx > kNegInf ? lb_pen(mx) : kNegInf;
     // the wave's 16 largest keys (0: no allowed token) to LDS
     uint32_t k16[1] = {lv > kNegInf ? ord32(lv) >> 16 : 0u};
     wave_sort_desc<1>(k16);
@@ -828,8 +858,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     // last wave: theta1 = the Kc-th largest of the posted keys.  They are
     // keys of distinct threads, so at least Kc threads reach it (exact
     // unless one wave held more than 16 of the Kc largest).
-    uint32_t t16 = 0;
-    const uint32_t r = (Kc - 1u) / kWave, l = (Kc - 1u) % kWave;
+    uint32_t t16;
     if (Kc <= (uint32_t)kWave) {
       uint32_t v[2];  // the 8 largest keys of each wave suffice
 #pragma unroll
@@ -837,24 +866,15 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
         const int e = q * kWave + lane;
         v[q] = sm.wtop[(e / 8) * kWTop + (e % 8)];
       }
-      wave_sort_desc<2>(v);
-      t16 = (uint32_t)__shfl((int)v[0], (int)l, kWave);
+      t16 = kth_key(v);
     } else {
       uint32_t v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = sm.wtop[q * kWave + lane];
-      wave_sort_desc<4>(v);
-      const uint32_t vr = r == 0 ? v[0] : v[1];  // Kc <= 128
-      t16 = (uint32_t)__shfl((int)vr, (int)l, kWave);
-    }
-    float t1 = t16 ? unord32(t16 << 16) : kNegInf;
-    if (t1 > kNegInf) {
-      // smallest raw x whose penalised value can reach t1
-      if (fa.use_pen && a.rho < 1.0f) t1 = t1 > 0.0f ? t1 * a.rho : t1 / a.rho;
-      t1 = t1 - __builtin_fabsf(t1) * 0x1p-12f - 0x1p-100f;
+      t16 = kth_key(v);
     }
     if (lane == 0) {
-      sm.theta_bits = f2u(t1);
+      sm.theta_ord = ord32(raw_of(t16));
       __hip_atomic_store(&sm.theta_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
@@ -866,7 +886,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       if (hv[q] >= 0) hist_bits(hv[q]);
     while (__hip_atomic_load(&sm.theta_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
       __builtin_amdgcn_s_sleep(1);
-    theta = u2f(__hip_atomic_load(&sm.theta_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    theta = unord32(__hip_atomic_load(&sm.theta_ord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
 #pragma unroll
     for (int q = 0; q < kNP; ++q) {
       const int64_t rel = (int64_t)q * kFT + tid;
@@ -877,7 +897,48 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       }
     }
   };
-  auto fold = [&](float(&x)[kFG][E], const uint32_t(&sw)[kFG], int64_t vbase, bool last) {
+  // Vectors whose maximum reaches theta are queued (raw, with their slice
+  // index) per wave and drained 64 at a time, one per lane, so the per-token
+  // tests run at full width however sparse the hits are.
+  const int wid = tid / kWave;
+  uint32_t qn = 0;  // wave-uniform queue length
+  auto drain = [&](uint32_t n) __attribute__((always_inline)) {
+    if ((uint32_t)lane < n) {
+      const u32x4 rv = sm.u.st.qv[wid][lane];
+      const uint32_t qi = sm.u.st.qi[wid][lane];
+      const int64_t vi = c.v0 + (qi >> 8);
+      const uint32_t ab = qi & 0xFFu;
+      float xv[E];
+      Vec<T>::cvt(rv, xv);
+      uint32_t cand = 0;
+#pragma unroll
+      for (int j = 0; j < E; ++j) cand |= (xv[j] >= theta && xv[j] > kNegInf ? 1u : 0u) << j;
+      cand &= ab;
+      while (cand) {
+        const int j = __builtin_ctz(cand);
+        cand &= cand - 1u;
+        float xj = xv[0];
+#pragma unroll
+        for (int q = 1; q < E; ++q) xj = q == j ? xv[q] : xj;
+        const uint32_t slot = atomicAdd(&sm.pool_n, 1u);
+        if (slot < (uint32_t)kCand) {
+          sm.ckey[slot] = (unsigned long long)(uint32_t)(vi * E + j);
+          sm.cx[slot] = xj;
+        }
+      }
+    }
+    // the rest (< 64 entries) moves to the front
+    const uint32_t rest = qn - n;
+    if ((uint32_t)lane < rest) {
+      const u32x4 t = sm.u.st.qv[wid][n + lane];
+      const uint32_t ti = sm.u.st.qi[wid][n + lane];
+      sm.u.st.qv[wid][lane] = t;
+      sm.u.st.qi[wid][lane] = ti;
+    }
+    qn = rest;
+  };
+  auto fold = [&](float(&x)[kFG][E], const u32x4(&raw)[kFG], uint32_t sw, int64_t vbase,
+                  bool last) {
     float gm[kFG];
 #pragma unroll
     for (int k = 0; k < kFG; ++k) gm[k] = vec_max<E>(x[k]);
@@ -895,15 +956,32 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     for (int k = 1; k + 1 < kFG; k += 2) cm = max3raw(cm, gm[k], gm[k + 1]);
     if (!(kFG & 1)) cm = max3raw(cm, gm[kFG - 1], gm[kFG - 1]);
     lse_fold_block_max<false, kFG, E>(st, x, cm);
-    if (cm >= theta) {
 #pragma unroll
-      for (int k = 0; k < kFG; ++k)
-        if (gm[k] >= theta) capture(x[k], sw[k], vbase + (int64_t)k * kWave);
+    for (int k = 0; k < kFG; ++k) {
+      const bool hit = gm[k] >= theta && gm[k] > kNegInf;
+      const unsigned long long m = __ballot(hit);
+      if (m) {
+        // this vector's allow bits: bit (o*E) & 31 of the chunk's word o*E >> 5
+        // (o = its offset in the chunk), held by that lane
+        uint32_t ab = (1u << E) - 1u;
+        if (kMask) {
+          const uint32_t o = (uint32_t)(k * kWave + lane) * E;
+          ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & ((1u << E) - 1u);
+        }
+        if (hit) {
+          const uint32_t pos = qn + (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
+          sm.u.st.qv[wid][pos] = raw[k];
+          sm.u.st.qi[wid][pos] = ((uint32_t)(vbase + (int64_t)k * kWave - c.v0) << 8) | ab;
+        }
+        qn += (uint32_t)__builtin_popcountll(m);
+        if (qn >= (uint32_t)kWave) drain((uint32_t)kWave);
+      }
     }
   };
   // non-temporal: the row is read once
-  stream_vectors_prefix<T, kFT, kNP, kFG, true, kMask>(
-      c.row, c.v0, c.v1, c.mrow, kMask ? (E == 8 ? 2 : 3) : 0, &sm.chunk_ctr, pre, post, fold);
+  stream_vectors_prefix<T, kFT, kNP, kFG, true, kMask>(c.row, c.v0, c.v1, c.mrow, &sm.chunk_ctr,
+                                                    pre, post, fold);
+  if (qn) drain(qn);
   // tokens past the last whole vector (last slice only)
   for (int64_t id = c.tail0 + tid; id < a.V; id += kFT) {
     float x[1][4] = {{Elem<T>::get(c.row, id), kNegInf, kNegInf, kNegInf}};
@@ -1032,11 +1110,11 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
           allowed += __builtin_popcount(mb);
         }
       }
-      sm.u.gkey[vi - c.v0] = (uint16_t)key;
+      sm.u.fb.gkey[vi - c.v0] = (uint16_t)key;
       rmax = max3raw(rmax, g, g);
     }
     // keys past the slice inside its last 16-byte chunk read as 0
-    if (tid < 8 && c.nv + tid < ((c.nv + 7) & ~7)) sm.u.gkey[c.nv + tid] = 0;
+    if (tid < 8 && c.nv + tid < ((c.nv + 7) & ~7)) sm.u.fb.gkey[c.nv + tid] = 0;
     uint32_t kmax;
     {
 #pragma unroll
@@ -1076,7 +1154,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       // large slices histogram a 1-in-8 sample of the keys (the threshold only
       // steers how many vectors are re-read; exactness is checked below)
       const bool sampled = c.nv > 8192;
-      const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.gkey);
+      const u32x4* keys = reinterpret_cast<const u32x4*>(sm.u.fb.gkey);
       const int nchunk = (c.nv + 7) >> 3;
       int shift = 0;
       for (int attempt = 0; attempt < 4; ++attempt) {
@@ -1254,7 +1332,8 @@ FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p,
   if (S > s_cap) S = s_cap;
   if (S < s_min) S = s_min;
   if (S < 1) S = 1;
-  const int64_t vps = (nvec + S - 1) / S;
+  // slices start on allow-mask word boundaries: vps a multiple of 8 vectors
+  const int64_t vps = ((nvec + S - 1) / S + 7) / 8 * 8;
   S = (nvec + vps - 1) / vps;
   pl.fast = true;
   pl.S = (int)S;

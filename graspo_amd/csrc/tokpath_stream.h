@@ -377,14 +377,22 @@ __device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, in
 // `post(p, sp, np)` runs with them in flight.  `pre` must not hold block
 // barriers: a wave that waits on another before issuing its own loads lets
 // the memory pipeline drain.  The rest of the range is streamed as in
-// stream_vectors_dyn: `fold(x, sw, vec_index, last)`, vector k of the block
-// at vec_index + k*64.
+// stream_vectors_dyn: `fold(x, raw, sw, vec_index, last)`, vector k of the
+// block (raw 16 bytes raw[k], converted x[k]) at vec_index + k*64.
+// With kSide, `side` is a bit array with one bit per element (E bits per
+// vector, bit i of word i >> 5): pilot vector v brings sp[q] = the word
+// holding its bits, and with each chunk lane l brings sw = word l of the
+// chunk's bits (the chunk's first element must be 32-aligned in `side`,
+// i.e. v0 + np a multiple of 32 / E; words past the range re-read the last
+// one).  Every load before the pilot is unconditional (out-of-range ones
+// re-read the first vector), so the compiler can wait for the pilot data
+// alone.
 template <typename T, int NT, int NP, int NG, bool kNonTemporal, bool kSide, typename Pre,
           typename Post, typename Fold>
 __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row, int64_t v0,
                                                       int64_t v1, const uint32_t* __restrict__ side,
-                                                      int side_shift, uint32_t* counter, Pre&& pre,
-                                                      Post&& post, Fold&& fold) {
+                                                      uint32_t* counter, Pre&& pre, Post&& post,
+                                                      Fold&& fold) {
   constexpr int E = Vec<T>::kE;
   constexpr uint32_t kChunk = (uint32_t)kWave * NG;
   const int64_t n = v1 - v0 > 0 ? v1 - v0 : 0;
@@ -400,13 +408,12 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
     vi = vi < (uint32_t)np ? vi : 0u;
     const u32x4* a = reinterpret_cast<const u32x4*>(base + vi * 16u);
     p[q] = kNonTemporal ? __builtin_nontemporal_load(a) : *a;
-    sp[q] = kSide ? side[(uint64_t)(v0 + vi) >> side_shift] : 0xFFFFFFFFu;
+    sp[q] = kSide ? side[((uint64_t)(v0 + vi) * E) >> 5] : 0xFFFFFFFFu;
   }
   pre(p, sp, np);
   // the rest: [v0 + np, v1) in per-wave chunks (an empty rest re-reads the
   // first vector of the range)
-  const int64_t off = np < n ? np : 0;
-  const char* __restrict__ base2 = base + off * 16;
+  const char* __restrict__ base2 = base + (np < n ? np : 0) * 16;
   const int64_t n2 = n - np;
   const uint32_t nchunks = (uint32_t)((n2 + kChunk - 1) / kChunk);
   const uint32_t last = n2 > 0 ? (uint32_t)(n2 - 1) : 0u;
@@ -415,9 +422,11 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
     if (lane == 0) c = atomicAdd(counter, 1u);
     return __builtin_amdgcn_readfirstlane(c);
   };
+  const uint64_t w_first = ((uint64_t)(v0 + (np < n ? np : 0)) * E) >> 5;
+  const uint64_t w_last = ((uint64_t)v1 * E - 1) >> 5;
   u32x4 a[NG], b[NG];
-  uint32_t sa[NG], sb[NG];
-  auto issue = [&](u32x4(&buf)[NG], uint32_t(&sbuf)[NG], uint32_t chunk) {
+  uint32_t swa = 0xFFFFFFFFu, swb = 0xFFFFFFFFu;
+  auto issue = [&](u32x4(&buf)[NG], uint32_t& sw, uint32_t chunk) {
     const bool live = chunk < nchunks;
     const uint32_t first = chunk * kChunk + lane;
 #pragma unroll
@@ -430,30 +439,33 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
         buf[k] = __builtin_nontemporal_load(q);
       else
         buf[k] = *q;
-      sbuf[k] = kSide ? side[(uint64_t)(v0 + off + vi) >> side_shift] : 0xFFFFFFFFu;
+    }
+    if (kSide) {
+      uint64_t w = w_first + (((uint64_t)(live ? chunk : 0u) * kChunk * E) >> 5) + lane;
+      sw = side[w < w_last ? w : w_last];
     }
   };
-  auto consume = [&](const u32x4(&buf)[NG], const uint32_t(&sbuf)[NG], uint32_t chunk) {
+  auto consume = [&](const u32x4(&buf)[NG], uint32_t sw, uint32_t chunk) {
     float x[NG][E];
 #pragma unroll
     for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
-    fold(x, sbuf, v0 + np + (int64_t)(chunk * kChunk + lane), chunk == nchunks - 1);
+    fold(x, buf, sw, v0 + np + (int64_t)(chunk * kChunk + lane), chunk == nchunks - 1);
   };
   uint32_t ca = grab();
-  issue(a, sa, ca);
+  issue(a, swa, ca);
   uint32_t cb = grab();
-  issue(b, sb, cb);
+  issue(b, swb, cb);
   post(p, sp, np);
   if (ca >= nchunks) return;
-  consume(a, sa, ca);
+  consume(a, swa, ca);
   while (cb < nchunks) {
     ca = grab();
-    issue(a, sa, ca);
-    consume(b, sb, cb);
+    issue(a, swa, ca);
+    consume(b, swb, cb);
     if (ca >= nchunks) break;
     cb = grab();
-    issue(b, sb, cb);
-    consume(a, sa, ca);
+    issue(b, swb, cb);
+    consume(a, swa, ca);
   }
 }
 
