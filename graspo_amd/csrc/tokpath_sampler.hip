@@ -36,6 +36,7 @@
 // Replaces _next_token_from_logits / _sample_next_token
 // (src/graspo/backends/graspoflow/tensor_utils.py:649-683).
 #include "tokpath_sampler_internal.h"
+#include "tokpath_stream.h"
 
 namespace gtp {
 
@@ -385,11 +386,10 @@ __device__ RadixResult radix_search(SamplerSmem& sm, const Row<T>& r, float m, b
 
 // ---------------------------------------------------------------- kernel
 
+// One row (block-uniform; every thread of the 1024-thread workgroup calls it).
 template <typename T>
-__global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
-  __shared__ SamplerSmem sm;
+__device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, SamplerSmem& sm) {
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.x;
 
   Row<T> r;
   r.x = reinterpret_cast<const T*>(a.logits) + b * a.row_stride;
@@ -879,6 +879,645 @@ __global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
   }
 }
 
+template <typename T>
+__global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
+  __shared__ SamplerSmem sm;
+  rowwise_row<T>(a, (int64_t)blockIdx.x, sm);
+}
+
+// ============================================================ value histogram
+//
+// Rows of bf16 logits with T > 0 on 16-byte aligned rows (top-p with or
+// without top-k, any top-k): every allowed, unpenalised token with the same
+// bf16 bit pattern has the same processed logit and the same fixed-point
+// weight, so the exact totals and prefix sums of the contract are sums over
+// the row's distinct values, not over its tokens.
+//
+// 1. One streaming pass (the only HBM read): the raw log-sum-exp, and a
+//    count per bf16 value (16384 bins: both signs, biased exponents
+//    [87, 151), i.e. 2^-40 <= |x| < 2^24).  Penalised tokens and values
+//    outside the bins are "singletons" kept with their raw value and id.
+// 2. m = the largest processed logit; per bin y = x / T and w = DETEXP_FIX(
+//    y - m); singletons get their exact y and w and join the segment (16
+//    bins, one per thread) whose value range holds them.  A block scan in
+//    descending order gives each segment the count and weight above it.
+// 3. The top-k rank, the top-p cut, the last kept rank and the draw each
+//    pick a segment from those totals; one wave resolves the order inside
+//    it (its bins in value order, its singletons sorted in registers and
+//    merged by position), where a run of equal values has equal weights, so
+//    positions inside it are integer quotients.
+// 4. A token of a bin is found by id: one rescan of the row counts the
+//    bin's tokens per thread range in id order.
+// Anything outside these bounds -- more singletons than the list holds, a
+// singleton exactly tied with a bin at a cut, more than 64 singletons in
+// one resolved segment, a non-finite processed logit -- runs the row-wise
+// path for the row instead, in the same workgroup.
+//
+// Replaces _sample_next_token (src/graspo/backends/graspoflow/tensor_utils.py:671-683)
+// for these rows.
+
+constexpr int kHBins = 16384;
+constexpr uint32_t kHELo = 87;
+constexpr int kHSegBins = kHBins / kSB;  // 16 bins per thread
+constexpr int kHSCap = 2560;             // singletons of a row
+constexpr int kHSegCap = 64;             // singletons of one resolved segment
+constexpr int kHG = 4;                   // vectors per thread per stream step
+
+struct HistSmem {
+  uint32_t cnt[kHBins];
+  uint32_t pen[GTP_SAMPLER_MAX_V / 32];
+  uint32_t sid[kHSCap];                  // id | penalised << 31
+  float sx[kHSCap];                      // raw logit
+  uint16_t sbin[kHSCap];                 // largest bin whose y <= the singleton's y (0xFFFF: none)
+  unsigned long long segw[kSB];          // singleton weight of each segment
+  uint32_t segc[kSB];
+  // segment resolution (wave 0)
+  unsigned long long it_w[kHSegBins + kHSegCap];  // per-token weight of each merged item
+  uint32_t it_c[kHSegBins + kHSegCap];            // tokens in the item
+  int32_t it_ref[kHSegBins + kHSegCap];           // bin index, or -1 - singleton slot
+  uint32_t sslot[kHSegCap];                       // singleton slots of the resolved segment
+  float red3[kSW][3];
+  uint32_t red_u[kSW];
+  uint32_t red_v[kSW];
+  unsigned long long red_w[kSW];
+  float red_m[kSW];
+  uint32_t ns;
+  uint32_t chunk_ctr;
+  int32_t seg_pick;
+  int32_t fallback;
+  uint32_t pick_c;
+  unsigned long long pick_w;
+  int32_t res_i[2];
+  unsigned long long res_w[2];
+  int32_t id_out[2];
+};
+
+// Block maximum of a float (every thread gets it).
+__device__ __forceinline__ float block_max_hist(HistSmem& sm, float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) sm.red_m[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float r = sm.red_m[0];
+#pragma unroll
+  for (int w = 1; w < kSW; ++w) r = fmaxf(r, sm.red_m[w]);
+  return r;
+}
+
+__device__ __forceinline__ int hbin_of(uint32_t h) {
+  const uint32_t mag = h & 0x7FFFu, e = mag >> 7;
+  if (e < kHELo || e >= kHELo + 64u) return -1;
+  const int idx = (int)(mag - (kHELo << 7));
+  return (h & 0x8000u) ? (kHBins / 2 - 1 - idx) : (kHBins / 2 + idx);
+}
+__device__ __forceinline__ uint32_t hbin_bits(int b) {
+  return b >= kHBins / 2 ? (uint32_t)(b - kHBins / 2) + (kHELo << 7)
+                         : 0x8000u | ((uint32_t)(kHBins / 2 - 1 - b) + (kHELo << 7));
+}
+
+// Position of the n-th (from 0) set bit of an 8-bit mask.
+__device__ __forceinline__ uint32_t nth_bit(uint32_t m, uint32_t n) {
+#pragma unroll
+  for (uint32_t i = 0; i < 8; ++i)
+    if (i < n) m &= m - 1u;
+  return (uint32_t)__builtin_ctz(m);
+}
+
+// wave sort of 64-bit keys, descending (one per lane)
+__device__ __forceinline__ unsigned long long wave_sort_desc_u64(unsigned long long v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      const unsigned long long w = __shfl_xor(v, j, kWave);
+      const bool desc = (lane & k) == 0;
+      const bool lower = (lane & j) == 0;
+      v = desc == lower ? (v > w ? v : w) : (v < w ? v : w);
+    }
+  }
+  return v;
+}
+
+// One row; false when the row needs the row-wise path instead.
+template <typename T, bool kMask>
+__device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSmem& sm) {
+  static_assert(sizeof(T) == 2, "bf16 rows only");
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  const T* __restrict__ row = reinterpret_cast<const T*>(a.logits) + b * a.row_stride;
+  const uint32_t* __restrict__ mrow = kMask ? a.mask + b * a.mask_stride : nullptr;
+  const int64_t V = a.V, nvec = V / 8;
+  const bool use_pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
+  const float Tc = a.T > 1e-6f ? a.T : 1e-6f;
+  const float u = a.uniforms[b];
+  auto yproc = [&](float x, bool pen) __attribute__((always_inline)) -> float {
+    float xp = x;
+    if (pen) xp = x < 0.0f ? x * a.rho : x / a.rho;
+    return xp / Tc + 0.0f;
+  };
+
+  // ---- 0. clear; penalty bitmap; history check
+  for (int i = tid; i < kHBins; i += kSB) sm.cnt[i] = 0u;
+  if (use_pen)
+    for (int i = tid; i < (int)((V + 31) / 32); i += kSB) sm.pen[i] = 0u;
+  sm.segw[tid] = 0ull;
+  sm.segc[tid] = 0u;
+  if (tid == 0) {
+    sm.ns = 0u;
+    sm.chunk_ctr = 0u;
+    sm.fallback = 0;
+  }
+  __syncthreads();
+  bool bad_hist = false;
+  if (a.hist && a.hist_len > 0) {
+    const int32_t* hr = a.hist + b * a.hist_stride;
+    for (int64_t j = tid; j < a.hist_len; j += kSB) {
+      const int32_t id = hr[j];
+      if (id >= V)
+        bad_hist = true;
+      else if (id >= 0 && use_pen)
+        atomicOr(&sm.pen[id >> 5], 1u << (id & 31));
+    }
+  }
+  bad_hist = __syncthreads_or(bad_hist);
+
+  // ---- 1. stream: raw log-sum-exp, value counts, singletons
+  Lse3 st{kNegInf, 0.0f, 0.0f};
+  auto classify = [&](int64_t id, uint32_t h, float x, bool pen) __attribute__((always_inline)) {
+    if (((h >> 7) & 0xFFu) == 0xFFu) return;  // -inf: never valid; NaN / +inf: row non-finite
+    const int bn = pen ? -1 : hbin_of(h);
+    if (bn >= 0) {
+      atomicAdd(&sm.cnt[bn], 1u);
+    } else {
+      const uint32_t slot = atomicAdd(&sm.ns, 1u);
+      if (slot < (uint32_t)kHSCap) {
+        sm.sid[slot] = (uint32_t)id | (pen ? 0x80000000u : 0u);
+        sm.sx[slot] = x;
+      }
+    }
+  };
+  auto fold = [&](float(&x)[kHG][8], const u32x4(&raw)[kHG], uint32_t sw, int64_t vbase,
+                  bool last) __attribute__((always_inline)) {
+    float gm[kHG];
+#pragma unroll
+    for (int k = 0; k < kHG; ++k) gm[k] = vec_max<8>(x[k]);
+    if (last) {
+#pragma unroll
+      for (int k = 0; k < kHG; ++k)
+        if (vbase + (int64_t)k * kWave >= nvec) {
+          gm[k] = kNegInf;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[k][j] = kNegInf;
+        }
+    }
+    float cm = gm[0];
+#pragma unroll
+    for (int k = 1; k + 1 < kHG; k += 2) cm = max3raw(cm, gm[k], gm[k + 1]);
+    if (!(kHG & 1)) cm = max3raw(cm, gm[kHG - 1], gm[kHG - 1]);
+    lse_fold_block_max<false, kHG, 8>(st, x, cm);
+#pragma unroll
+    for (int k = 0; k < kHG; ++k) {
+      const int64_t vi = vbase + (int64_t)k * kWave;
+      uint32_t ab = 0xFFu;
+      if (kMask) {
+        const uint32_t o = (uint32_t)(k * kWave + lane) * 8u;
+        ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & 0xFFu;
+      }
+      if (last && vi >= nvec) ab = 0u;
+      const uint32_t pb = use_pen && ab ? (sm.pen[(uint32_t)((vi * 8) >> 5)] >> ((vi * 8) & 31)) & 0xFFu : 0u;
+      const uint32_t wds[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if ((ab >> j) & 1u)
+          classify(vi * 8 + j, (j & 1) ? (wds[j >> 1] >> 16) : (wds[j >> 1] & 0xFFFFu), x[k][j],
+                   (pb >> j) & 1u);
+    }
+  };
+  stream_chunks<T, kHG, false, kMask>(row, 0, nvec, mrow, &sm.chunk_ctr, fold);
+  for (int64_t id = nvec * 8 + tid; id < V; id += kSB) {
+    const float xv = Elem<T>::get(row, id);
+    float x1[1][4] = {{xv, kNegInf, kNegInf, kNegInf}};
+    lse_fold_block_max<false, 1, 4>(st, x1, xv);
+    const bool allowed = !kMask || ((mrow[id >> 5] >> (id & 31)) & 1u);
+    const bool pen = use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
+    if (allowed) classify(id, f2u(xv) >> 16, xv, pen);
+  }
+  float lm = st.m, ls = st.s;
+  block_lse2<kSB>(lm, ls, sm.red3);  // its barrier completes the counts and singletons
+  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+  int32_t status = GTP_ROW_OK;
+  if (ls != ls || lm == kPosInf)
+    status = GTP_ROW_NONFINITE;
+  else if (bad_hist)
+    status = GTP_ROW_BAD_HISTORY;
+  else if (!(u >= 0.0f && u < 1.0f))
+    status = GTP_ROW_BAD_UNIFORM;
+  if (status != GTP_ROW_OK) {
+    if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
+    return true;
+  }
+  const uint32_t ns = sm.ns;
+  if (ns > (uint32_t)kHSCap) return false;
+  auto ybin = [&](int bn) __attribute__((always_inline)) -> float { return u2f(hbin_bits(bn) << 16) / Tc + 0.0f; };
+
+  // ---- 2. m, per-segment count and weight, singletons placed
+  const int seg0 = tid * kHSegBins;
+  uint32_t C_t = 0;
+  int top_b = -1;
+#pragma unroll
+  for (int q = 0; q < kHSegBins; ++q) {
+    const uint32_t c = sm.cnt[seg0 + q];
+    C_t += c;
+    if (c) top_b = seg0 + q;
+  }
+  float ymax = top_b >= 0 ? ybin(top_b) : kNegInf;
+  bool odd = false;
+  for (uint32_t s = tid; s < ns; s += kSB) {
+    const float y = yproc(sm.sx[s], sm.sid[s] >> 31);
+    odd |= !(y > kNegInf && y < kPosInf);
+    ymax = fmaxf(ymax, y);
+  }
+  if (__syncthreads_or(odd)) return false;
+  const float m = block_max_hist(sm, ymax);
+  unsigned long long W_t = 0;
+#pragma unroll
+  for (int q = 0; q < kHSegBins; ++q) {
+    const uint32_t c = sm.cnt[seg0 + q];
+    if (c) W_t += (unsigned long long)c * detexp_fix(ybin(seg0 + q) - m);
+  }
+  for (uint32_t s = tid; s < ns; s += kSB) {
+    const float y = yproc(sm.sx[s], sm.sid[s] >> 31);
+    int lo = 0, hi = kHBins - 1, bf = -1;  // largest bin with y(bin) <= y
+    while (lo <= hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ybin(mid) <= y) {
+        bf = mid;
+        lo = mid + 1;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
+    const int sg = bf < 0 ? 0 : bf / kHSegBins;
+    atomicAdd(&sm.segw[sg], detexp_fix(y - m));
+    atomicAdd(&sm.segc[sg], 1u);
+  }
+  __syncthreads();
+  W_t += sm.segw[tid];
+  C_t += sm.segc[tid];
+  // weight / count of all segments above this one (descending order)
+  unsigned long long aW;
+  uint32_t aC;
+  unsigned long long W_all;
+  uint32_t n_valid;
+  {
+    unsigned long long iw = W_t;
+    uint32_t ic = C_t;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const unsigned long long w = __shfl_down(iw, o, kWave);
+      const uint32_t cc = (uint32_t)__shfl_down((int)ic, o, kWave);
+      if (lane + o < kWave) {
+        iw += w;
+        ic += cc;
+      }
+    }
+    if (lane == 0) {
+      sm.red_w[wid] = iw;
+      sm.red_u[wid] = ic;
+    }
+    __syncthreads();
+    unsigned long long hw = 0;
+    uint32_t hc = 0;
+    W_all = 0;
+    n_valid = 0;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w) {
+      if (w > wid) {
+        hw += sm.red_w[w];
+        hc += sm.red_u[w];
+      }
+      W_all += sm.red_w[w];
+      n_valid += sm.red_u[w];
+    }
+    aW = hw + iw - W_t;
+    aC = hc + ic - C_t;
+  }
+  if (n_valid == 0u) {
+    if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
+    return true;
+  }
+
+  // ---- 3. searches.  pick(): the segment whose interval holds the target
+  // (its count and weight above broadcast with it).
+  auto pick = [&](bool mine) __attribute__((always_inline)) {
+    __syncthreads();
+    if (tid == 0) sm.seg_pick = -1;
+    __syncthreads();
+    if (mine) {
+      sm.seg_pick = tid;
+      sm.pick_c = aC;
+      sm.pick_w = aW;
+    }
+    __syncthreads();
+  };
+  // Resolve segment t (wave 0): its items (nonzero bins and singletons) in
+  // rank order.  mode 0: the item holding in-segment rank v; mode 1: the
+  // item holding in-segment weight offset v; mode 2: the number of
+  // in-segment ranks whose preceding weight is <= v.  Results in
+  // sm.res_i = {item ref (bin, or -1 - singleton slot), index in the item or
+  // the count} and sm.res_w = {weight before the item, per-token weight}.
+  // Returns false (block-uniform) when the segment is outside its bounds.
+  auto resolve = [&](int t, int mode, unsigned long long v) __attribute__((always_inline)) -> bool {
+    __syncthreads();
+    if (wid == 0) {
+      const int b0 = t * kHSegBins;
+      uint32_t k = 0;
+      for (uint32_t base = 0; base < ns; base += kWave) {
+        const uint32_t s = base + (uint32_t)lane;
+        bool in = false;
+        if (s < ns) {
+          const uint32_t sb = sm.sbin[s];
+          in = (sb == 0xFFFFu ? 0 : (int)sb / kHSegBins) == t;
+        }
+        const unsigned long long mk = __ballot(in);
+        const uint32_t pos = k + (uint32_t)__builtin_popcountll(mk & ((1ull << lane) - 1ull));
+        if (in && pos < (uint32_t)kHSegCap) sm.sslot[pos] = s;
+        k += (uint32_t)__builtin_popcountll(mk);
+      }
+      bool bad = k > (uint32_t)kHSegCap;
+      // the singletons sorted by rank: key = (ord y, ~(id << 12 | slot))
+      unsigned long long key = 0;
+      if (!bad && (uint32_t)lane < k) {
+        const uint32_t sl = sm.sslot[lane];
+        const uint32_t sv = sm.sid[sl];
+        const float y = yproc(sm.sx[sl], sv >> 31);
+        key = ((unsigned long long)ord32(y) << 32) |
+              (unsigned long long)(0xFFFFFFFFu - (((sv & 0x7FFFFFFFu) << 12) | sl));
+      }
+      key = wave_sort_desc_u64(key);
+      const bool have = !bad && (uint32_t)lane < k;
+      const uint32_t s_me = have ? (0xFFFFFFFFu - (uint32_t)key) & 0xFFFu : 0u;
+      const float y_me = have ? unord32((uint32_t)(key >> 32)) : kNegInf;
+      const int sb_me = have ? (sm.sbin[s_me] == 0xFFFFu ? -1 : (int)sm.sbin[s_me]) : -1;
+      uint32_t nb_above = 0;
+      bool tie = false;
+      if (have) {
+#pragma unroll
+        for (int q = 0; q < kHSegBins; ++q)
+          if (b0 + q > sb_me && sm.cnt[b0 + q]) ++nb_above;
+        tie = sb_me >= b0 && sm.cnt[sb_me] && ybin(sb_me) == y_me;
+      }
+      bad |= __ballot(tie) != 0ull;
+      if (!bad) {
+        if (have) {
+          const uint32_t pos = (uint32_t)lane + nb_above;
+          sm.it_w[pos] = detexp_fix(y_me - m);
+          sm.it_c[pos] = 1u;
+          sm.it_ref[pos] = -1 - (int32_t)s_me;
+        }
+        uint32_t nzb = 0;
+        for (int q = kHSegBins - 1; q >= 0; --q) {
+          const int bq = b0 + q;
+          const uint32_t c = sm.cnt[bq];
+          const unsigned long long above_s = __ballot(have && sb_me >= bq);
+          if (c) {
+            if (lane == 0) {
+              const uint32_t pos = nzb + (uint32_t)__builtin_popcountll(above_s);
+              sm.it_w[pos] = detexp_fix(ybin(bq) - m);
+              sm.it_c[pos] = c;
+              sm.it_ref[pos] = bq;
+            }
+            ++nzb;
+          }
+        }
+        const uint32_t n_it = nzb + k;
+        uint32_t c2[2] = {0u, 0u};
+        unsigned long long w2[2] = {0ull, 0ull}, wt2[2] = {0ull, 0ull};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t i = 2u * (uint32_t)lane + (uint32_t)q;
+          if (i < n_it) {
+            c2[q] = sm.it_c[i];
+            w2[q] = sm.it_w[i];
+            wt2[q] = (unsigned long long)c2[q] * w2[q];
+          }
+        }
+        const uint32_t lc = c2[0] + c2[1];
+        const unsigned long long lw = wt2[0] + wt2[1];
+        uint32_t cin = lc;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t cc = (uint32_t)__shfl_up((int)cin, o, kWave);
+          if (lane >= o) cin += cc;
+        }
+        uint32_t cb = cin - lc;
+        unsigned long long wb = wave_incl_scan_u64(lw) - lw;
+        uint32_t count = 0;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t i = 2u * (uint32_t)lane + (uint32_t)q;
+          if (i < n_it) {
+            bool hit = false;
+            uint32_t jj = 0;
+            if (mode == 0) {
+              hit = v >= cb && v < (unsigned long long)cb + c2[q];
+              jj = (uint32_t)(v - cb);
+            } else if (mode == 1) {
+              hit = v >= wb && v < wb + wt2[q];
+              jj = w2[q] ? (uint32_t)((v - wb) / w2[q]) : 0u;
+            } else if (v >= wb) {
+              const unsigned long long f = w2[q] ? (v - wb) / w2[q] + 1ull : (unsigned long long)c2[q];
+              count += f < c2[q] ? (uint32_t)f : c2[q];
+            }
+            if (hit) {
+              sm.res_i[0] = sm.it_ref[i];
+              sm.res_i[1] = (int32_t)jj;
+              sm.res_w[0] = wb;
+              sm.res_w[1] = w2[q];
+            }
+            cb += c2[q];
+            wb += wt2[q];
+          }
+        }
+        if (mode == 2) {
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) count += (uint32_t)__shfl_xor((int)count, o, kWave);
+          if (lane == 0) sm.res_i[1] = (int32_t)count;
+        }
+      }
+      if (lane == 0) sm.fallback = bad ? 1 : 0;
+    }
+    __syncthreads();
+    return sm.fallback == 0;
+  };
+  const bool p_active = a.P > 0.0f && a.P < 1.0f;
+  const bool k_active = a.K >= 1 && (uint32_t)a.K < n_valid;
+  const uint32_t nk = k_active ? (uint32_t)a.K : n_valid;
+  // Four searches over the rank order, one resolved segment each:
+  // (0) top-k: W_K = S_nk, the weight of the nk best ranks (S_r: the weight
+  //     of the ranks before r);
+  // (1) top-p: R = min(nk, #{r : S_r <= floor(P W_K)});
+  // (2) the last kept rank R - 1, and W' = S_R;
+  // (3) the draw: the rank whose weight interval holds U = floor(u W').
+  unsigned long long W_K = W_all, Wp = 0;
+  uint32_t R = nk;
+  int32_t thr_ref = 0, thr_j = 0, drw_ref = 0, drw_j = 0;
+  unsigned long long w_draw = 0;
+  for (int step = 0; step < 4; ++step) {
+    if ((step == 0 && !k_active) || (step == 1 && !p_active)) continue;
+    const int mode = step == 1 ? 2 : step == 3 ? 1 : 0;
+    const unsigned long long target = step == 0   ? (unsigned long long)(nk - 1u)
+                                      : step == 1 ? floor_mul(a.P, W_K)
+                                      : step == 2 ? (unsigned long long)(R - 1u)
+                                                  : floor_mul(u, Wp);
+    pick(mode == 0 ? (C_t && aC <= target && target < (unsigned long long)aC + C_t)
+                   : (W_t && aW <= target && target < aW + W_t));
+    if (sm.seg_pick < 0) return false;
+    if (!resolve(sm.seg_pick, mode, target - (mode == 0 ? sm.pick_c : sm.pick_w))) return false;
+    const unsigned long long S_after =
+        sm.pick_w + sm.res_w[0] + (unsigned long long)(sm.res_i[1] + 1) * sm.res_w[1];
+    if (step == 0) {
+      W_K = S_after;
+    } else if (step == 1) {
+      const uint32_t le = sm.pick_c + (uint32_t)sm.res_i[1];
+      R = le < nk ? le : nk;
+    } else if (step == 2) {
+      thr_ref = sm.res_i[0];
+      thr_j = sm.res_i[1];
+      Wp = S_after;
+    } else {
+      drw_ref = sm.res_i[0];
+      drw_j = sm.res_i[1];
+      w_draw = sm.res_w[1];
+    }
+  }
+
+  // ---- 4. ids: a singleton's is known; a bin's is the j-th token (in id
+  // order) with that value among the allowed, unpenalised ones.  Wave w
+  // scans a contiguous range of vectors, lanes on consecutive vectors; a bin
+  // of one token takes the first match, else per-wave counts pick the wave
+  // that walks its range again to the j-th match.
+  const uint32_t h1 = thr_ref >= 0 ? hbin_bits(thr_ref) : 0x10000u;  // 0x10000: matches nothing
+  const uint32_t h2 = drw_ref >= 0 ? hbin_bits(drw_ref) : 0x10000u;
+  const bool one1 = thr_ref >= 0 && sm.cnt[thr_ref] == 1u;
+  const bool one2 = drw_ref >= 0 && sm.cnt[drw_ref] == 1u;
+  __syncthreads();
+  if (tid == 0) {
+    sm.id_out[0] = thr_ref < 0 ? (int32_t)(sm.sid[-1 - thr_ref] & 0x7FFFFFFFu) : -1;
+    sm.id_out[1] = drw_ref < 0 ? (int32_t)(sm.sid[-1 - drw_ref] & 0x7FFFFFFFu) : -1;
+  }
+  if (thr_ref >= 0 || drw_ref >= 0) {
+    const int64_t nv8 = (V + 7) / 8;
+    const int64_t vpw = (nv8 + kSW - 1) / kSW;
+    const int64_t w0 = (int64_t)wid * vpw < nv8 ? (int64_t)wid * vpw : nv8;
+    const int64_t w1 = w0 + vpw < nv8 ? w0 + vpw : nv8;
+    // 8-bit masks of the members of vector vi for h1 (low byte) and h2
+    auto match = [&](int64_t vi) __attribute__((always_inline)) -> uint32_t {
+      uint32_t hv[8];
+      const int64_t e0 = vi * 8;
+      if (e0 + 8 <= V) {
+        const u32x4 r = *reinterpret_cast<const u32x4*>(row + e0);
+        const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = e0 + j < V ? (uint32_t)row[e0 + j] : 0x10001u;
+      }
+      uint32_t m1 = 0, m2 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        m1 |= (hv[j] == h1 ? 1u : 0u) << j;
+        m2 |= (hv[j] == h2 ? 1u : 0u) << j;
+      }
+      uint32_t ok = 0xFFu;
+      if (kMask) ok &= (mrow[e0 >> 5] >> (e0 & 31)) & 0xFFu;
+      if (use_pen) ok &= ~(sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu;
+      return (m1 & ok) | ((m2 & ok) << 8);
+    };
+    uint32_t c1 = 0, c2 = 0;
+    for (int64_t vi = w0 + lane; vi < w1; vi += kWave) {
+      const uint32_t mm = match(vi);
+      c1 += (uint32_t)__builtin_popcount(mm & 0xFFu);
+      c2 += (uint32_t)__builtin_popcount(mm >> 8);
+      if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)(vi * 8 + __builtin_ctz(mm & 0xFFu));
+      if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)(vi * 8 + __builtin_ctz(mm >> 8));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      c1 += (uint32_t)__shfl_xor((int)c1, o, kWave);
+      c2 += (uint32_t)__shfl_xor((int)c2, o, kWave);
+    }
+    __syncthreads();
+    if (lane == 0) {
+      sm.red_u[wid] = c1;
+      sm.red_v[wid] = c2;
+    }
+    __syncthreads();
+    uint32_t p1 = 0, p2 = 0;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w)
+      if (w < wid) {
+        p1 += sm.red_u[w];
+        p2 += sm.red_v[w];
+      }
+    // the waves holding the j-th member walk their range again
+    const bool walk1 = thr_ref >= 0 && !one1 && (uint32_t)thr_j >= p1 && (uint32_t)thr_j < p1 + c1;
+    const bool walk2 = drw_ref >= 0 && !one2 && (uint32_t)drw_j >= p2 && (uint32_t)drw_j < p2 + c2;
+    if (walk1 || walk2) {
+      uint32_t base1 = p1, base2 = p2;
+      for (int64_t v0 = w0; v0 < w1; v0 += kWave) {
+        const int64_t vi = v0 + lane;
+        const uint32_t mm = vi < w1 ? match(vi) : 0u;
+        const uint32_t n1 = walk1 ? (uint32_t)__builtin_popcount(mm & 0xFFu) : 0u;
+        const uint32_t n2 = walk2 ? (uint32_t)__builtin_popcount(mm >> 8) : 0u;
+        uint32_t i1 = n1, i2 = n2;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t x1 = (uint32_t)__shfl_up((int)i1, o, kWave);
+          const uint32_t x2 = (uint32_t)__shfl_up((int)i2, o, kWave);
+          if (lane >= o) {
+            i1 += x1;
+            i2 += x2;
+          }
+        }
+        const uint32_t e1 = base1 + i1 - n1, e2 = base2 + i2 - n2;
+        if (walk1 && (uint32_t)thr_j >= e1 && (uint32_t)thr_j < e1 + n1)
+          sm.id_out[0] = (int32_t)(vi * 8 + nth_bit(mm & 0xFFu, (uint32_t)thr_j - e1));
+        if (walk2 && (uint32_t)drw_j >= e2 && (uint32_t)drw_j < e2 + n2)
+          sm.id_out[1] = (int32_t)(vi * 8 + nth_bit(mm >> 8, (uint32_t)drw_j - e2));
+        base1 += (uint32_t)__shfl((int)i1, kWave - 1, kWave);
+        base2 += (uint32_t)__shfl((int)i2, kWave - 1, kWave);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t id_thr = sm.id_out[0], id_draw = sm.id_out[1];
+    const float y_thr = thr_ref >= 0 ? ybin(thr_ref)
+                                     : yproc(sm.sx[-1 - thr_ref], sm.sid[-1 - thr_ref] >> 31);
+    const float x_draw = drw_ref >= 0 ? u2f(hbin_bits(drw_ref) << 16) : sm.sx[-1 - drw_ref];
+    const float slp = (float)::log((double)w_draw / (double)Wp);
+    write_row(a, b, GTP_ROW_OK, id_draw, x_draw - lse_raw, slp, (int32_t)R, y_thr, id_thr);
+  }
+  return true;
+}
+
+template <typename T, bool kMask>
+__global__ __launch_bounds__(kSB) void sampler_hist_kernel(SamplerArgs a) {
+  __shared__ union {
+    HistSmem h;
+    SamplerSmem g;
+  } smu;
+  const int64_t b = blockIdx.x;
+  if (!hist_row<T, kMask>(a, b, smu.h)) {
+    __syncthreads();
+    rowwise_row<T>(a, b, smu.g);
+  }
+}
+
 }  // namespace gtp
 
 using namespace gtp;
@@ -889,6 +1528,19 @@ namespace gtp {
 // and parameter combination the contract allows.
 int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s) {
   const dim3 grid((unsigned)B), block(kSB);
+  // bf16 sampling rows on 16-byte aligned rows take the value-histogram
+  // kernel (temperature bounded so that distinct bf16 values keep distinct,
+  // normal y = x / T)
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0 &&
+                       ((a.row_stride * 2) & 15) == 0;
+  const bool use_pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
+  if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f && !use_pen) {
+    if (a.mask)
+      hipLaunchKernelGGL((sampler_hist_kernel<uint16_t, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((sampler_hist_kernel<uint16_t, false>), grid, block, 0, s, a);
+    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+  }
   switch (dtype) {
     case GTP_DTYPE_BF16:
       hipLaunchKernelGGL(sampler_rowwise_kernel<uint16_t>, grid, block, 0, s, a);

@@ -138,19 +138,6 @@ static_assert(sizeof(FastSmem) <= 160 * 1024, "one workgroup per CU");
 
 // ------------------------------------------------------------------ helpers
 
-template <int E>
-__device__ __forceinline__ float vec_max(const float (&x)[E]) {
-  if constexpr (E == 8) {
-    float m = max3raw(x[0], x[1], x[2]);
-    m = max3raw(m, x[3], x[4]);
-    m = max3raw(m, x[5], x[6]);
-    return max3raw(m, x[7], x[7]);
-  } else {
-    const float m = max3raw(x[0], x[1], x[2]);
-    return max3raw(m, x[3], x[3]);
-  }
-}
-
 // Order key of a vector maximum: its bf16 rounding toward +inf.
 template <typename T>
 __device__ __forceinline__ uint32_t vec_key(float gm) {

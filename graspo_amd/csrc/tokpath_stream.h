@@ -34,6 +34,20 @@ __device__ __forceinline__ float max3raw(float a, float b, float c) {
   return d;
 }
 
+// maximum of one vector's E logits (same NaN rule as max3raw)
+template <int E>
+__device__ __forceinline__ float vec_max(const float (&x)[E]) {
+  if constexpr (E == 8) {
+    float m = max3raw(x[0], x[1], x[2]);
+    m = max3raw(m, x[3], x[4]);
+    m = max3raw(m, x[5], x[6]);
+    return max3raw(m, x[7], x[7]);
+  } else {
+    const float m = max3raw(x[0], x[1], x[2]);
+    return max3raw(m, x[3], x[3]);
+  }
+}
+
 // One 16-byte vector of logits.
 template <typename T>
 struct Vec;
@@ -466,6 +480,69 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
     cb = grab();
     issue(b, swb, cb);
     consume(a, swa, ca);
+  }
+}
+
+// Per-wave dynamic chunks of 64 x NG vectors over [v0, v1) (v1 > v0), as the
+// main loop of stream_vectors_prefix: `fold(x, raw, sw, vec_index, last)`;
+// with kSide lane l also brings word l of the chunk's bits in `side` (one bit
+// per element; v0 * E must be a multiple of 32).
+template <typename T, int NG, bool kNonTemporal, bool kSide, typename Fold>
+__device__ __forceinline__ void stream_chunks(const T* __restrict__ row, int64_t v0, int64_t v1,
+                                              const uint32_t* __restrict__ side,
+                                              uint32_t* counter, Fold&& fold) {
+  constexpr int E = Vec<T>::kE;
+  constexpr uint32_t kChunk = (uint32_t)kWave * NG;
+  const int64_t n = v1 - v0 > 0 ? v1 - v0 : 0;
+  const char* __restrict__ base = reinterpret_cast<const char*>(row) + v0 * 16;
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const uint32_t nchunks = (uint32_t)((n + kChunk - 1) / kChunk);
+  const uint32_t last = n > 0 ? (uint32_t)(n - 1) : 0u;
+  const uint64_t w_first = ((uint64_t)v0 * E) >> 5;
+  const uint64_t w_last = n > 0 ? ((uint64_t)v1 * E - 1) >> 5 : w_first;
+  auto grab = [&]() -> uint32_t {
+    uint32_t c = 0;
+    if (lane == 0) c = atomicAdd(counter, 1u);
+    return __builtin_amdgcn_readfirstlane(c);
+  };
+  u32x4 a[NG], b[NG];
+  uint32_t swa = 0xFFFFFFFFu, swb = 0xFFFFFFFFu;
+  auto issue = [&](u32x4(&buf)[NG], uint32_t& sw, uint32_t chunk) {
+    const bool live = chunk < nchunks;
+    const uint32_t first = chunk * kChunk + lane;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      uint32_t vi = first + (uint32_t)k * kWave;
+      vi = vi < last ? vi : last;
+      vi = live ? vi : 0u;
+      const u32x4* q = reinterpret_cast<const u32x4*>(base + vi * 16u);
+      if (kNonTemporal)
+        buf[k] = __builtin_nontemporal_load(q);
+      else
+        buf[k] = *q;
+    }
+    if (kSide) {
+      const uint64_t w = w_first + (((uint64_t)(live ? chunk : 0u) * kChunk * E) >> 5) + lane;
+      sw = side[w < w_last ? w : w_last];
+    }
+  };
+  auto consume = [&](const u32x4(&buf)[NG], uint32_t sw, uint32_t chunk) {
+    float x[NG][E];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
+    fold(x, buf, sw, v0 + (int64_t)(chunk * kChunk + lane), chunk == nchunks - 1);
+  };
+  if (n == 0) return;
+  uint32_t ca = grab();
+  issue(a, swa, ca);
+  while (ca < nchunks) {
+    const uint32_t cb = grab();
+    issue(b, swb, cb);
+    consume(a, swa, ca);
+    if (cb >= nchunks) break;
+    ca = grab();
+    issue(a, swa, ca);
+    consume(b, swb, cb);
   }
 }
 
