@@ -888,54 +888,64 @@ __global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
 // ============================================================ value histogram
 //
 // Rows of bf16 logits with T > 0 on 16-byte aligned rows (top-p with or
-// without top-k, any top-k): every allowed, unpenalised token with the same
-// bf16 bit pattern has the same processed logit and the same fixed-point
-// weight, so the exact totals and prefix sums of the contract are sums over
-// the row's distinct values, not over its tokens.
+// without top-k, any top-k): all allowed tokens with the same bf16 bit
+// pattern and the same penalty state have the same processed logit and the
+// same fixed-point weight, so the exact totals and prefix sums of the
+// contract are sums over the row's distinct values, not over its tokens.
 //
-// 1. One streaming pass (the only HBM read): the raw log-sum-exp, and a
-//    count per bf16 value (16384 bins: both signs, biased exponents
-//    [87, 151), i.e. 2^-40 <= |x| < 2^24).  Penalised tokens and values
-//    outside the bins are "singletons" kept with their raw value and id.
-// 2. m = the largest processed logit; per bin y = x / T and w = DETEXP_FIX(
-//    y - m); singletons get their exact y and w and join the segment (16
-//    bins, one per thread) whose value range holds them.  A block scan in
-//    descending order gives each segment the count and weight above it.
+// 1. One streaming pass (the only full HBM read): the raw log-sum-exp, and
+//    a count per bf16 value (16384 bins: both signs, biased exponents
+//    [87, 151), i.e. 2^-40 <= |x| < 2^24).  Values outside the bins are
+//    "singletons" kept with their raw value and id.  Afterwards each
+//    distinct penalised history id moves from its value's count to a second
+//    count per value (penalised values: y = pen(x) / T).
+// 2. m = the largest processed logit.  A segment is 16 value bins (one per
+//    thread); each penalised value and each singleton joins the segment
+//    whose value range holds its y.  A block scan in descending order gives
+//    each segment the count and weight above it.
 // 3. The top-k rank, the top-p cut, the last kept rank and the draw each
 //    pick a segment from those totals; one wave resolves the order inside
-//    it (its bins in value order, its singletons sorted in registers and
-//    merged by position), where a run of equal values has equal weights, so
-//    positions inside it are integer quotients.
+//    it: its bins in value order, its extra items (penalised values and
+//    singletons, sorted in registers) merged by position, and a penalised
+//    value equal to a bin's y merged into that bin.  A run of tokens with
+//    one value has one weight, so positions inside it are integer quotients.
 // 4. A token of a bin is found by id: one rescan of the row counts the
-//    bin's tokens per thread range in id order.
+//    bin's tokens per thread range, in id order.
 // Anything outside these bounds -- more singletons than the list holds, a
-// singleton exactly tied with a bin at a cut, more than 64 singletons in
-// one resolved segment, a non-finite processed logit -- runs the row-wise
-// path for the row instead, in the same workgroup.
+// singleton or penalised value exactly tied with another item at a cut,
+// more than 64 extra items in one resolved segment, a non-finite processed
+// logit -- runs the row-wise path for the row instead, in the same
+// workgroup.
 //
 // Replaces _sample_next_token (src/graspo/backends/graspoflow/tensor_utils.py:671-683)
 // for these rows.
 
 constexpr int kHBins = 16384;
 constexpr uint32_t kHELo = 87;
-constexpr int kHSegBins = kHBins / kSB;  // 16 bins per thread
-constexpr int kHSCap = 2560;             // singletons of a row
-constexpr int kHSegCap = 64;             // singletons of one resolved segment
+constexpr int kHSegBins = kHBins / kSB;  // 16 bins per thread and per segment
+constexpr int kHSCap = 1024;             // singletons of a row
+constexpr int kHXCap = 64;               // extra items of one resolved segment
+constexpr int kHItems = kHSegBins + kHXCap;
+constexpr int kHPenSpan = 2048;          // penalised-value bins one segment may span
 constexpr int kHG = 4;                   // vectors per thread per stream step
+constexpr uint32_t kNoPattern = 0x10000u;  // matches no 16-bit pattern
 
-struct HistSmem {
-  uint32_t cnt[kHBins];
-  uint32_t pen[GTP_SAMPLER_MAX_V / 32];
-  uint32_t sid[kHSCap];                  // id | penalised << 31
-  float sx[kHSCap];                      // raw logit
+struct alignas(16) HistSmem {
+  uint32_t cnt[kHBins + kWave];          // allowed unpenalised tokens per value (+ a spill word per lane)
+  uint32_t pcnt2[kHBins / 2];            // allowed penalised tokens per value, 16 bits each
+  uint32_t pen[GTP_SAMPLER_MAX_V / 32];  // penalised ids
+  uint32_t sid[kHSCap];                  // singleton id
+  float sx[kHSCap];                      // singleton raw logit
   uint16_t sbin[kHSCap];                 // largest bin whose y <= the singleton's y (0xFFFF: none)
-  unsigned long long segw[kSB];          // singleton weight of each segment
+  unsigned long long segw[kSB];          // weight of the extra items of each segment
   uint32_t segc[kSB];
-  // segment resolution (wave 0)
-  unsigned long long it_w[kHSegBins + kHSegCap];  // per-token weight of each merged item
-  uint32_t it_c[kHSegBins + kHSegCap];            // tokens in the item
-  int32_t it_ref[kHSegBins + kHSegCap];           // bin index, or -1 - singleton slot
-  uint32_t sslot[kHSegCap];                       // singleton slots of the resolved segment
+  // the resolved segment (wave 0)
+  unsigned long long it_w[kHItems];      // per-token weight of each item, in rank order
+  uint32_t it_c[kHItems];                // tokens in the item
+  int32_t it_ref[kHItems];               // bin b, kHBins + penalised bin p, or -1 - singleton slot
+  int32_t it_aux[kHItems];               // penalised bin merged into bin b, or -1
+  uint32_t xcode[kHXCap];                // extra items: kHBins + p, or singleton slot
+  int32_t aux_q[kHSegBins];
   float red3[kSW][3];
   uint32_t red_u[kSW];
   uint32_t red_v[kSW];
@@ -947,10 +957,12 @@ struct HistSmem {
   int32_t fallback;
   uint32_t pick_c;
   unsigned long long pick_w;
-  int32_t res_i[2];
-  unsigned long long res_w[2];
+  int32_t res_ref, res_aux, res_j;
+  uint32_t res_c;
+  unsigned long long res_wb, res_w;
   int32_t id_out[2];
 };
+static_assert(sizeof(HistSmem) <= 160 * 1024, "one workgroup per CU");
 
 // Block maximum of a float (every thread gets it).
 __device__ __forceinline__ float block_max_hist(HistSmem& sm, float v) {
@@ -975,6 +987,9 @@ __device__ __forceinline__ uint32_t hbin_bits(int b) {
   return b >= kHBins / 2 ? (uint32_t)(b - kHBins / 2) + (kHELo << 7)
                          : 0x8000u | ((uint32_t)(kHBins / 2 - 1 - b) + (kHELo << 7));
 }
+__device__ __forceinline__ uint32_t pcnt_of(const HistSmem& sm, int p) {
+  return (sm.pcnt2[p >> 1] >> ((p & 1) * 16)) & 0xFFFFu;
+}
 
 // Position of the n-th (from 0) set bit of an 8-bit mask.
 __device__ __forceinline__ uint32_t nth_bit(uint32_t m, uint32_t n) {
@@ -982,6 +997,53 @@ __device__ __forceinline__ uint32_t nth_bit(uint32_t m, uint32_t n) {
   for (uint32_t i = 0; i < 8; ++i)
     if (i < n) m &= m - 1u;
   return (uint32_t)__builtin_ctz(m);
+}
+
+// Orders one wave's LDS writes before its later LDS reads from other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lane l receives lane l - s of its row of 16 (row_shr), lane 15 of the
+// previous row (row_bcast:15, rows 1 and 3) or lane 31 (row_bcast:31, rows
+// 2 and 3); lanes without a source read 0.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_take(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xF, false);
+}
+// Inclusive scans over the 64 lanes of a wave (DPP, no LDS round trip).
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  x += dpp_take<0x111, 0xF>(x);
+  x += dpp_take<0x112, 0xF>(x);
+  x += dpp_take<0x114, 0xF>(x);
+  x += dpp_take<0x118, 0xF>(x);
+  x += dpp_take<0x142, 0xA>(x);
+  x += dpp_take<0x143, 0xC>(x);
+  return x;
+}
+__device__ __forceinline__ unsigned long long wave_scan_u64(unsigned long long x) {
+#define GTP_SCAN64_STEP(ctrl, rm)                                                    \
+  {                                                                                  \
+    const uint32_t lo = dpp_take<ctrl, rm>((uint32_t)x);                             \
+    const uint32_t hi = dpp_take<ctrl, rm>((uint32_t)(x >> 32));                     \
+    x += ((unsigned long long)hi << 32) | lo;                                        \
+  }
+  GTP_SCAN64_STEP(0x111, 0xF)
+  GTP_SCAN64_STEP(0x112, 0xF)
+  GTP_SCAN64_STEP(0x114, 0xF)
+  GTP_SCAN64_STEP(0x118, 0xF)
+  GTP_SCAN64_STEP(0x142, 0xA)
+  GTP_SCAN64_STEP(0x143, 0xC)
+#undef GTP_SCAN64_STEP
+  return x;
+}
+__device__ __forceinline__ uint32_t lane63_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
+}
+__device__ __forceinline__ unsigned long long lane63_u64(unsigned long long v) {
+  return ((unsigned long long)lane63_u32((uint32_t)(v >> 32)) << 32) | lane63_u32((uint32_t)v);
 }
 
 // wave sort of 64-bit keys, descending (one per lane)
@@ -1010,51 +1072,68 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   const int64_t V = a.V, nvec = V / 8;
   const bool use_pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
   const float Tc = a.T > 1e-6f ? a.T : 1e-6f;
+  const float rho = a.rho;
   const float u = a.uniforms[b];
-  auto yproc = [&](float x, bool pen) __attribute__((always_inline)) -> float {
-    float xp = x;
-    if (pen) xp = x < 0.0f ? x * a.rho : x / a.rho;
+  auto ybin = [&](int bn) __attribute__((always_inline)) -> float {
+    return u2f(hbin_bits(bn) << 16) / Tc + 0.0f;
+  };
+  auto ypen = [&](float x) __attribute__((always_inline)) -> float {
+    const float xp = x < 0.0f ? x * rho : x / rho;
     return xp / Tc + 0.0f;
   };
+  auto ypbin = [&](int p) __attribute__((always_inline)) -> float {
+    return ypen(u2f(hbin_bits(p) << 16));
+  };
+  auto is_pen = [&](int64_t id) __attribute__((always_inline)) -> bool {
+    return use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
+  };
+  auto allowed = [&](int64_t id) __attribute__((always_inline)) -> bool {
+    return !kMask || ((mrow[id >> 5] >> (id & 31)) & 1u);
+  };
+  // largest bin whose y <= y (-1: none): from the bin of y * T (within a
+  // bin or two of the answer), else by bisection
+  auto place = [&](float y) __attribute__((always_inline)) -> int {
+    int g = hbin_of(f2u(y * Tc) >> 16);
+    if (g >= 0) {
+      while (g + 1 < kHBins && ybin(g + 1) <= y) ++g;
+      while (g >= 0 && ybin(g) > y) --g;
+      return g;
+    }
+    int lo = 0, hi = kHBins - 1, bf = -1;
+    while (lo <= hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ybin(mid) <= y) {
+        bf = mid;
+        lo = mid + 1;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    return bf;
+  };
 
-  // ---- 0. clear; penalty bitmap; history check
-  for (int i = tid; i < kHBins; i += kSB) sm.cnt[i] = 0u;
+  // ---- 0. clear
+  for (int i = tid; i < kHBins + kWave; i += kSB) sm.cnt[i] = 0u;
+  for (int i = tid; i < kHBins / 2; i += kSB) sm.pcnt2[i] = 0u;
   if (use_pen)
     for (int i = tid; i < (int)((V + 31) / 32); i += kSB) sm.pen[i] = 0u;
   sm.segw[tid] = 0ull;
   sm.segc[tid] = 0u;
+  if (tid < kHSegBins) sm.aux_q[tid] = -1;
   if (tid == 0) {
     sm.ns = 0u;
     sm.chunk_ctr = 0u;
     sm.fallback = 0;
   }
   __syncthreads();
-  bool bad_hist = false;
-  if (a.hist && a.hist_len > 0) {
-    const int32_t* hr = a.hist + b * a.hist_stride;
-    for (int64_t j = tid; j < a.hist_len; j += kSB) {
-      const int32_t id = hr[j];
-      if (id >= V)
-        bad_hist = true;
-      else if (id >= 0 && use_pen)
-        atomicOr(&sm.pen[id >> 5], 1u << (id & 31));
-    }
-  }
-  bad_hist = __syncthreads_or(bad_hist);
 
   // ---- 1. stream: raw log-sum-exp, value counts, singletons
   Lse3 st{kNegInf, 0.0f, 0.0f};
-  auto classify = [&](int64_t id, uint32_t h, float x, bool pen) __attribute__((always_inline)) {
-    if (((h >> 7) & 0xFFu) == 0xFFu) return;  // -inf: never valid; NaN / +inf: row non-finite
-    const int bn = pen ? -1 : hbin_of(h);
-    if (bn >= 0) {
-      atomicAdd(&sm.cnt[bn], 1u);
-    } else {
-      const uint32_t slot = atomicAdd(&sm.ns, 1u);
-      if (slot < (uint32_t)kHSCap) {
-        sm.sid[slot] = (uint32_t)id | (pen ? 0x80000000u : 0u);
-        sm.sx[slot] = x;
-      }
+  auto single = [&](int64_t id, float x) __attribute__((always_inline)) {
+    const uint32_t slot = atomicAdd(&sm.ns, 1u);
+    if (slot < (uint32_t)kHSCap) {
+      sm.sid[slot] = (uint32_t)id;
+      sm.sx[slot] = x;
     }
   };
   auto fold = [&](float(&x)[kHG][8], const u32x4(&raw)[kHG], uint32_t sw, int64_t vbase,
@@ -1085,13 +1164,22 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & 0xFFu;
       }
       if (last && vi >= nvec) ab = 0u;
-      const uint32_t pb = use_pen && ab ? (sm.pen[(uint32_t)((vi * 8) >> 5)] >> ((vi * 8) & 31)) & 0xFFu : 0u;
       const uint32_t wds[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+      uint32_t sg = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if ((ab >> j) & 1u)
-          classify(vi * 8 + j, (j & 1) ? (wds[j >> 1] >> 16) : (wds[j >> 1] & 0xFFFFu), x[k][j],
-                   (pb >> j) & 1u);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t h = (j & 1) ? (wds[j >> 1] >> 16) : (wds[j >> 1] & 0xFFFFu);
+        const int bn = hbin_of(h);
+        const bool ok = (ab >> j) & 1u;
+        // tokens outside the bins and masked tokens count in the lane's spill word
+        atomicAdd(&sm.cnt[ok && bn >= 0 ? bn : kHBins + lane], 1u);
+        sg |= (ok && bn < 0 && ((h >> 7) & 0xFFu) != 0xFFu) ? (1u << j) : 0u;
+      }
+      if (sg) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if ((sg >> j) & 1u) single(vi * 8 + j, x[k][j]);
+      }
     }
   };
   stream_chunks<T, kHG, false, kMask>(row, 0, nvec, mrow, &sm.chunk_ctr, fold);
@@ -1099,13 +1187,42 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     const float xv = Elem<T>::get(row, id);
     float x1[1][4] = {{xv, kNegInf, kNegInf, kNegInf}};
     lse_fold_block_max<false, 1, 4>(st, x1, xv);
-    const bool allowed = !kMask || ((mrow[id >> 5] >> (id & 31)) & 1u);
-    const bool pen = use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
-    if (allowed) classify(id, f2u(xv) >> 16, xv, pen);
+    if (allowed(id)) {
+      const uint32_t h = f2u(xv) >> 16;
+      const int bn = hbin_of(h);
+      if (bn >= 0)
+        atomicAdd(&sm.cnt[bn], 1u);
+      else if (((h >> 7) & 0xFFu) != 0xFFu)
+        single(id, xv);
+    }
   }
   float lm = st.m, ls = st.s;
   block_lse2<kSB>(lm, ls, sm.red3);  // its barrier completes the counts and singletons
   const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+
+  // ---- history: each distinct, allowed penalised id moves to the
+  // penalised count of its value (singletons read the bitmap later)
+  bool bad_hist = false;
+  if (a.hist && a.hist_len > 0) {
+    const int32_t* hr = a.hist + b * a.hist_stride;
+    for (int64_t j = tid; j < a.hist_len; j += kSB) {
+      const int32_t id = hr[j];
+      if (id >= V) {
+        bad_hist = true;
+      } else if (id >= 0 && use_pen) {
+        const uint32_t bit = 1u << (id & 31);
+        const uint32_t old = atomicOr(&sm.pen[id >> 5], bit);
+        if (!(old & bit) && allowed(id)) {
+          const int bn = hbin_of((uint32_t)row[id]);
+          if (bn >= 0) {
+            atomicSub(&sm.cnt[bn], 1u);
+            atomicAdd(&sm.pcnt2[bn >> 1], 1u << ((bn & 1) * 16));
+          }
+        }
+      }
+    }
+  }
+  bad_hist = __syncthreads_or(bad_hist);
   int32_t status = GTP_ROW_OK;
   if (ls != ls || lm == kPosInf)
     status = GTP_ROW_NONFINITE;
@@ -1119,22 +1236,52 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   }
   const uint32_t ns = sm.ns;
   if (ns > (uint32_t)kHSCap) return false;
-  auto ybin = [&](int bn) __attribute__((always_inline)) -> float { return u2f(hbin_bits(bn) << 16) / Tc + 0.0f; };
 
-  // ---- 2. m, per-segment count and weight, singletons placed
+  // ---- 2. m, per-segment count and weight, extra items placed
   const int seg0 = tid * kHSegBins;
+  uint32_t cu[kHSegBins], cp[kHSegBins];
+  {
+    const u32x4* c4 = reinterpret_cast<const u32x4*>(sm.cnt + seg0);
+    const u32x4* p4 = reinterpret_cast<const u32x4*>(sm.pcnt2 + seg0 / 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = c4[i];
+      cu[4 * i] = v.x;
+      cu[4 * i + 1] = v.y;
+      cu[4 * i + 2] = v.z;
+      cu[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 v = p4[i];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        cp[8 * i + 2 * k] = w[k] & 0xFFFFu;
+        cp[8 * i + 2 * k + 1] = w[k] >> 16;
+      }
+    }
+  }
   uint32_t C_t = 0;
-  int top_b = -1;
+  int top_u = -1;
+  float ypq[kHSegBins];
+  bool odd = false;
+  float ymax = kNegInf;
 #pragma unroll
   for (int q = 0; q < kHSegBins; ++q) {
-    const uint32_t c = sm.cnt[seg0 + q];
-    C_t += c;
-    if (c) top_b = seg0 + q;
+    C_t += cu[q];
+    if (cu[q]) top_u = q;
+    ypq[q] = kNegInf;
+    if (cp[q]) {
+      ypq[q] = ypbin(seg0 + q);
+      odd |= !(ypq[q] > kNegInf && ypq[q] < kPosInf);
+      ymax = fmaxf(ymax, ypq[q]);
+    }
   }
-  float ymax = top_b >= 0 ? ybin(top_b) : kNegInf;
-  bool odd = false;
+  if (top_u >= 0) ymax = fmaxf(ymax, ybin(seg0 + top_u));
   for (uint32_t s = tid; s < ns; s += kSB) {
-    const float y = yproc(sm.sx[s], sm.sid[s] >> 31);
+    const float x = sm.sx[s];
+    const float y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
     odd |= !(y > kNegInf && y < kPosInf);
     ymax = fmaxf(ymax, y);
   }
@@ -1142,22 +1289,22 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   const float m = block_max_hist(sm, ymax);
   unsigned long long W_t = 0;
 #pragma unroll
+  for (int q = 0; q < kHSegBins; ++q)
+    if (cu[q]) W_t += (unsigned long long)cu[q] * detexp_fix(ybin(seg0 + q) - m);
+#pragma unroll
   for (int q = 0; q < kHSegBins; ++q) {
-    const uint32_t c = sm.cnt[seg0 + q];
-    if (c) W_t += (unsigned long long)c * detexp_fix(ybin(seg0 + q) - m);
+    if (cp[q]) {
+      const float y = ypq[q];
+      const int bf = place(y);
+      const int sg = bf < 0 ? 0 : bf / kHSegBins;
+      atomicAdd(&sm.segw[sg], (unsigned long long)cp[q] * detexp_fix(y - m));
+      atomicAdd(&sm.segc[sg], cp[q]);
+    }
   }
   for (uint32_t s = tid; s < ns; s += kSB) {
-    const float y = yproc(sm.sx[s], sm.sid[s] >> 31);
-    int lo = 0, hi = kHBins - 1, bf = -1;  // largest bin with y(bin) <= y
-    while (lo <= hi) {
-      const int mid = (lo + hi) >> 1;
-      if (ybin(mid) <= y) {
-        bf = mid;
-        lo = mid + 1;
-      } else {
-        hi = mid - 1;
-      }
-    }
+    const float x = sm.sx[s];
+    const float y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
+    const int bf = place(y);
     sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
     const int sg = bf < 0 ? 0 : bf / kHSegBins;
     atomicAdd(&sm.segw[sg], detexp_fix(y - m));
@@ -1166,26 +1313,17 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   __syncthreads();
   W_t += sm.segw[tid];
   C_t += sm.segc[tid];
-  // weight / count of all segments above this one (descending order)
-  unsigned long long aW;
-  uint32_t aC;
-  unsigned long long W_all;
-  uint32_t n_valid;
+  // count / weight of all segments above this one (descending order)
+  unsigned long long aW, W_all;
+  uint32_t aC, n_valid;
   {
-    unsigned long long iw = W_t;
-    uint32_t ic = C_t;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const unsigned long long w = __shfl_down(iw, o, kWave);
-      const uint32_t cc = (uint32_t)__shfl_down((int)ic, o, kWave);
-      if (lane + o < kWave) {
-        iw += w;
-        ic += cc;
-      }
-    }
+    const unsigned long long iw = wave_scan_u64(W_t);
+    const uint32_t ic = wave_scan_u32(C_t);
+    const unsigned long long tw = lane63_u64(iw);
+    const uint32_t tc = lane63_u32(ic);
     if (lane == 0) {
-      sm.red_w[wid] = iw;
-      sm.red_u[wid] = ic;
+      sm.red_w[wid] = tw;
+      sm.red_u[wid] = tc;
     }
     __syncthreads();
     unsigned long long hw = 0;
@@ -1201,8 +1339,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       W_all += sm.red_w[w];
       n_valid += sm.red_u[w];
     }
-    aW = hw + iw - W_t;
-    aC = hc + ic - C_t;
+    aW = hw + (tw - iw);
+    aC = hc + (tc - ic);
   }
   if (n_valid == 0u) {
     if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
@@ -1222,76 +1360,165 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     }
     __syncthreads();
   };
-  // Resolve segment t (wave 0): its items (nonzero bins and singletons) in
-  // rank order.  mode 0: the item holding in-segment rank v; mode 1: the
-  // item holding in-segment weight offset v; mode 2: the number of
-  // in-segment ranks whose preceding weight is <= v.  Results in
-  // sm.res_i = {item ref (bin, or -1 - singleton slot), index in the item or
-  // the count} and sm.res_w = {weight before the item, per-token weight}.
-  // Returns false (block-uniform) when the segment is outside its bounds.
-  auto resolve = [&](int t, int mode, unsigned long long v) __attribute__((always_inline)) -> bool {
+  // Resolve segment t (wave 0): its items in rank order.  mode 0: the item
+  // holding in-segment rank v; mode 1: the item holding in-segment weight
+  // offset v; mode 2: the number of in-segment ranks whose preceding weight
+  // is <= v (in res_j).  Returns false (block-uniform) when the segment is
+  // outside the bounds of this path.
+  auto resolve = [&](int t, int mode, unsigned long long v)
+                     __attribute__((always_inline)) -> bool {
     __syncthreads();
     if (wid == 0) {
       const int b0 = t * kHSegBins;
-      uint32_t k = 0;
-      for (uint32_t base = 0; base < ns; base += kWave) {
-        const uint32_t s = base + (uint32_t)lane;
-        bool in = false;
-        if (s < ns) {
-          const uint32_t sb = sm.sbin[s];
-          in = (sb == 0xFFFFu ? 0 : (int)sb / kHSegBins) == t;
-        }
-        const unsigned long long mk = __ballot(in);
-        const uint32_t pos = k + (uint32_t)__builtin_popcountll(mk & ((1ull << lane) - 1ull));
-        if (in && pos < (uint32_t)kHSegCap) sm.sslot[pos] = s;
-        k += (uint32_t)__builtin_popcountll(mk);
-      }
-      bool bad = k > (uint32_t)kHSegCap;
-      // the singletons sorted by rank: key = (ord y, ~(id << 12 | slot))
-      unsigned long long key = 0;
-      if (!bad && (uint32_t)lane < k) {
-        const uint32_t sl = sm.sslot[lane];
-        const uint32_t sv = sm.sid[sl];
-        const float y = yproc(sm.sx[sl], sv >> 31);
-        key = ((unsigned long long)ord32(y) << 32) |
-              (unsigned long long)(0xFFFFFFFFu - (((sv & 0x7FFFFFFFu) << 12) | sl));
-      }
-      key = wave_sort_desc_u64(key);
-      const bool have = !bad && (uint32_t)lane < k;
-      const uint32_t s_me = have ? (0xFFFFFFFFu - (uint32_t)key) & 0xFFFu : 0u;
-      const float y_me = have ? unord32((uint32_t)(key >> 32)) : kNegInf;
-      const int sb_me = have ? (sm.sbin[s_me] == 0xFFFFu ? -1 : (int)sm.sbin[s_me]) : -1;
-      uint32_t nb_above = 0;
-      bool tie = false;
-      if (have) {
+      bool bad = false;
+      // the segment's bins, as scalars
+      float ys[kHSegBins];
+      uint32_t cs[kHSegBins];
+      {
+        const float yl = lane < kHSegBins ? ybin(b0 + lane) : 0.0f;
+        const uint32_t cl = lane < kHSegBins ? sm.cnt[b0 + lane] : 0u;
 #pragma unroll
-        for (int q = 0; q < kHSegBins; ++q)
-          if (b0 + q > sb_me && sm.cnt[b0 + q]) ++nb_above;
-        tie = sb_me >= b0 && sm.cnt[sb_me] && ybin(sb_me) == y_me;
+        for (int q = 0; q < kHSegBins; ++q) {
+          ys[q] = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(yl), q));
+          cs[q] = (uint32_t)__builtin_amdgcn_readlane((int)cl, q);
+        }
       }
-      bad |= __ballot(tie) != 0ull;
+      // penalised values placed here: [plo, phi), found by bisection
+      int plo = 0, phi = 0;
+      if (use_pen) {
+        int r = 0;
+        if (lane < 2) {
+          if (lane == 0 && t == 0) {
+            r = 0;
+          } else if (lane == 1 && t == kSB - 1) {
+            r = kHBins;
+          } else {
+            const float yt = ybin(b0 + kHSegBins * lane);
+            int lo = 0, hi = kHBins;
+            while (lo < hi) {
+              const int mid = (lo + hi) >> 1;
+              if (ypbin(mid) >= yt)
+                hi = mid;
+              else
+                lo = mid + 1;
+            }
+            r = lo;
+          }
+        }
+        plo = __builtin_amdgcn_readlane(r, 0);
+        phi = __builtin_amdgcn_readlane(r, 1);
+        if (phi - plo > kHPenSpan) bad = true;
+      }
+      // extra items: penalised values not equal to a bin with tokens, and
+      // the segment's singletons
+      uint32_t k = 0;
+      if (!bad) {
+        for (int base = plo; base < phi; base += kWave) {
+          const int p = base + lane;
+          bool ext = false;
+          if (p < phi && pcnt_of(sm, p)) {
+            const float y = ypbin(p);
+            int tq = -1;
+#pragma unroll
+            for (int q = 0; q < kHSegBins; ++q)
+              if (cs[q] && ys[q] == y) tq = q;
+            if (tq >= 0)
+              sm.aux_q[tq] = p;
+            else
+              ext = true;
+          }
+          const unsigned long long mk = __ballot(ext);
+          const uint32_t pos = k + (uint32_t)__builtin_popcountll(mk & ((1ull << lane) - 1ull));
+          if (ext && pos < (uint32_t)kHXCap) sm.xcode[pos] = (uint32_t)(kHBins + p);
+          k += (uint32_t)__builtin_popcountll(mk);
+        }
+        for (uint32_t base = 0; base < ns; base += kWave) {
+          const uint32_t s = base + (uint32_t)lane;
+          bool in = false;
+          if (s < ns) {
+            const uint32_t sb = sm.sbin[s];
+            in = (sb == 0xFFFFu ? 0 : (int)sb / kHSegBins) == t;
+          }
+          const unsigned long long mk = __ballot(in);
+          const uint32_t pos = k + (uint32_t)__builtin_popcountll(mk & ((1ull << lane) - 1ull));
+          if (in && pos < (uint32_t)kHXCap) sm.xcode[pos] = s;
+          k += (uint32_t)__builtin_popcountll(mk);
+        }
+        bad = k > (uint32_t)kHXCap;
+      }
+      // extras sorted by rank: key = (ord y, ~tag), tag = id << 12 | slot for
+      // a singleton, 2^30 | p for a penalised value
+      const bool have = !bad && (uint32_t)lane < k;
+      unsigned long long key = 0;
+      if (have) {
+        const uint32_t code = sm.xcode[lane];
+        float y;
+        uint32_t tag;
+        if (code >= (uint32_t)kHBins) {
+          const int p = (int)code - kHBins;
+          y = ypbin(p);
+          tag = 0x40000000u | (uint32_t)p;
+        } else {
+          const uint32_t id = sm.sid[code];
+          const float x = sm.sx[code];
+          y = is_pen(id) ? ypen(x) : x / Tc + 0.0f;
+          tag = (id << 12) | code;
+        }
+        key = ((unsigned long long)ord32(y) << 32) | (unsigned long long)(0xFFFFFFFFu - tag);
+      }
+      wave_lds_sync();  // xcode and aux_q, written above, are read below
+      if (k > 1u && !bad) key = wave_sort_desc_u64(key);
+      const uint32_t tag_me = 0xFFFFFFFFu - (uint32_t)key;
+      const uint32_t oy_me = (uint32_t)(key >> 32);
+      const float y_me = have ? unord32(oy_me) : kNegInf;
+      const bool pen_item = have && (tag_me & 0x40000000u);
+      // ties that the item order cannot express
+      {
+        const uint32_t oy_next = (uint32_t)__shfl_down((int)oy_me, 1, kWave);
+        const bool pen_next = __shfl_down((int)pen_item, 1, kWave) != 0;
+        bool tie = have && (uint32_t)lane + 1u < k && oy_next == oy_me && (pen_item || pen_next);
+        if (have && !pen_item) {
+#pragma unroll
+          for (int q = 0; q < kHSegBins; ++q)
+            if (cs[q] && ys[q] == y_me) tie = true;
+        }
+        bad |= __ballot(tie) != 0ull;
+      }
       if (!bad) {
         if (have) {
+          uint32_t nb_above = 0;
+#pragma unroll
+          for (int q = 0; q < kHSegBins; ++q)
+            if (cs[q] && ys[q] > y_me) ++nb_above;
           const uint32_t pos = (uint32_t)lane + nb_above;
           sm.it_w[pos] = detexp_fix(y_me - m);
-          sm.it_c[pos] = 1u;
-          sm.it_ref[pos] = -1 - (int32_t)s_me;
+          if (pen_item) {
+            const int p = (int)(tag_me & 0x3FFFFu);
+            sm.it_c[pos] = pcnt_of(sm, p);
+            sm.it_ref[pos] = kHBins + p;
+          } else {
+            sm.it_c[pos] = 1u;
+            sm.it_ref[pos] = -1 - (int32_t)(tag_me & 0xFFFu);
+          }
+          sm.it_aux[pos] = -1;
         }
         uint32_t nzb = 0;
+#pragma unroll
         for (int q = kHSegBins - 1; q >= 0; --q) {
-          const int bq = b0 + q;
-          const uint32_t c = sm.cnt[bq];
-          const unsigned long long above_s = __ballot(have && sb_me >= bq);
-          if (c) {
+          const unsigned long long above_x = __ballot(have && y_me > ys[q]);
+          if (cs[q]) {
             if (lane == 0) {
-              const uint32_t pos = nzb + (uint32_t)__builtin_popcountll(above_s);
-              sm.it_w[pos] = detexp_fix(ybin(bq) - m);
-              sm.it_c[pos] = c;
-              sm.it_ref[pos] = bq;
+              const uint32_t pos = nzb + (uint32_t)__builtin_popcountll(above_x);
+              const int32_t ax = sm.aux_q[q];
+              sm.it_w[pos] = detexp_fix(ys[q] - m);
+              sm.it_c[pos] = cs[q] + (ax >= 0 ? pcnt_of(sm, ax) : 0u);
+              sm.it_ref[pos] = b0 + q;
+              sm.it_aux[pos] = ax;
             }
             ++nzb;
           }
         }
+        wave_lds_sync();
         const uint32_t n_it = nzb + k;
         uint32_t c2[2] = {0u, 0u};
         unsigned long long w2[2] = {0ull, 0ull}, wt2[2] = {0ull, 0ull};
@@ -1306,14 +1533,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         }
         const uint32_t lc = c2[0] + c2[1];
         const unsigned long long lw = wt2[0] + wt2[1];
-        uint32_t cin = lc;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-          const uint32_t cc = (uint32_t)__shfl_up((int)cin, o, kWave);
-          if (lane >= o) cin += cc;
-        }
-        uint32_t cb = cin - lc;
-        unsigned long long wb = wave_incl_scan_u64(lw) - lw;
+        uint32_t cb = wave_scan_u32(lc) - lc;
+        unsigned long long wb = wave_scan_u64(lw) - lw;
         uint32_t count = 0;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -1328,25 +1549,28 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
               hit = v >= wb && v < wb + wt2[q];
               jj = w2[q] ? (uint32_t)((v - wb) / w2[q]) : 0u;
             } else if (v >= wb) {
-              const unsigned long long f = w2[q] ? (v - wb) / w2[q] + 1ull : (unsigned long long)c2[q];
+              const unsigned long long f =
+                  w2[q] ? (v - wb) / w2[q] + 1ull : (unsigned long long)c2[q];
               count += f < c2[q] ? (uint32_t)f : c2[q];
             }
             if (hit) {
-              sm.res_i[0] = sm.it_ref[i];
-              sm.res_i[1] = (int32_t)jj;
-              sm.res_w[0] = wb;
-              sm.res_w[1] = w2[q];
+              sm.res_ref = sm.it_ref[i];
+              sm.res_aux = sm.it_aux[i];
+              sm.res_j = (int32_t)jj;
+              sm.res_c = c2[q];
+              sm.res_wb = wb;
+              sm.res_w = w2[q];
             }
             cb += c2[q];
             wb += wt2[q];
           }
         }
         if (mode == 2) {
-#pragma unroll
-          for (int o = 32; o > 0; o >>= 1) count += (uint32_t)__shfl_xor((int)count, o, kWave);
-          if (lane == 0) sm.res_i[1] = (int32_t)count;
+          count = lane63_u32(wave_scan_u32(count));
+          if (lane == 0) sm.res_j = (int32_t)count;
         }
       }
+      if (lane < kHSegBins) sm.aux_q[lane] = -1;
       if (lane == 0) sm.fallback = bad ? 1 : 0;
     }
     __syncthreads();
@@ -1361,10 +1585,10 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   // (1) top-p: R = min(nk, #{r : S_r <= floor(P W_K)});
   // (2) the last kept rank R - 1, and W' = S_R;
   // (3) the draw: the rank whose weight interval holds U = floor(u W').
-  unsigned long long W_K = W_all, Wp = 0;
+  unsigned long long W_K = W_all, Wp = 0, w_draw = 0;
   uint32_t R = nk;
-  int32_t thr_ref = 0, thr_j = 0, drw_ref = 0, drw_j = 0;
-  unsigned long long w_draw = 0;
+  int32_t thr_ref = 0, thr_aux = -1, thr_j = 0, drw_ref = 0, drw_aux = -1, drw_j = 0;
+  uint32_t thr_c = 0, drw_c = 0;
   for (int step = 0; step < 4; ++step) {
     if ((step == 0 && !k_active) || (step == 1 && !p_active)) continue;
     const int mode = step == 1 ? 2 : step == 3 ? 1 : 0;
@@ -1377,128 +1601,174 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     if (sm.seg_pick < 0) return false;
     if (!resolve(sm.seg_pick, mode, target - (mode == 0 ? sm.pick_c : sm.pick_w))) return false;
     const unsigned long long S_after =
-        sm.pick_w + sm.res_w[0] + (unsigned long long)(sm.res_i[1] + 1) * sm.res_w[1];
+        sm.pick_w + sm.res_wb + (unsigned long long)(sm.res_j + 1) * sm.res_w;
     if (step == 0) {
       W_K = S_after;
     } else if (step == 1) {
-      const uint32_t le = sm.pick_c + (uint32_t)sm.res_i[1];
+      const uint32_t le = sm.pick_c + (uint32_t)sm.res_j;
       R = le < nk ? le : nk;
     } else if (step == 2) {
-      thr_ref = sm.res_i[0];
-      thr_j = sm.res_i[1];
+      thr_ref = sm.res_ref;
+      thr_aux = sm.res_aux;
+      thr_j = sm.res_j;
+      thr_c = sm.res_c;
       Wp = S_after;
     } else {
-      drw_ref = sm.res_i[0];
-      drw_j = sm.res_i[1];
-      w_draw = sm.res_w[1];
+      drw_ref = sm.res_ref;
+      drw_aux = sm.res_aux;
+      drw_j = sm.res_j;
+      drw_c = sm.res_c;
+      w_draw = sm.res_w;
     }
   }
 
-  // ---- 4. ids: a singleton's is known; a bin's is the j-th token (in id
-  // order) with that value among the allowed, unpenalised ones.  Wave w
-  // scans a contiguous range of vectors, lanes on consecutive vectors; a bin
-  // of one token takes the first match, else per-wave counts pick the wave
-  // that walks its range again to the j-th match.
-  const uint32_t h1 = thr_ref >= 0 ? hbin_bits(thr_ref) : 0x10000u;  // 0x10000: matches nothing
-  const uint32_t h2 = drw_ref >= 0 ? hbin_bits(drw_ref) : 0x10000u;
-  const bool one1 = thr_ref >= 0 && sm.cnt[thr_ref] == 1u;
-  const bool one2 = drw_ref >= 0 && sm.cnt[drw_ref] == 1u;
+  // ---- 4. ids: a singleton's is known; otherwise the j-th token, in id
+  // order, among the allowed tokens with the item's bit pattern (unpenalised
+  // for a bin, penalised for a penalised value; both for a merged bin).
+  // Thread t scans a contiguous range of vectors; a one-token item takes the
+  // first match, else per-thread counts pick the thread that walks its
+  // range again to the j-th match.
+  uint32_t hu1 = kNoPattern, hp1 = kNoPattern, hu2 = kNoPattern, hp2 = kNoPattern;
+  if (thr_ref >= kHBins) {
+    hp1 = hbin_bits(thr_ref - kHBins);
+  } else if (thr_ref >= 0) {
+    hu1 = hbin_bits(thr_ref);
+    if (thr_aux >= 0) hp1 = hbin_bits(thr_aux);
+  }
+  if (drw_ref >= kHBins) {
+    hp2 = hbin_bits(drw_ref - kHBins);
+  } else if (drw_ref >= 0) {
+    hu2 = hbin_bits(drw_ref);
+    if (drw_aux >= 0) hp2 = hbin_bits(drw_aux);
+  }
+  const bool need1 = thr_ref >= 0, need2 = drw_ref >= 0;
+  const bool one1 = need1 && thr_c == 1u, one2 = need2 && drw_c == 1u;
   __syncthreads();
   if (tid == 0) {
-    sm.id_out[0] = thr_ref < 0 ? (int32_t)(sm.sid[-1 - thr_ref] & 0x7FFFFFFFu) : -1;
-    sm.id_out[1] = drw_ref < 0 ? (int32_t)(sm.sid[-1 - drw_ref] & 0x7FFFFFFFu) : -1;
+    sm.id_out[0] = need1 ? -1 : (int32_t)sm.sid[-1 - thr_ref];
+    sm.id_out[1] = need2 ? -1 : (int32_t)sm.sid[-1 - drw_ref];
   }
-  if (thr_ref >= 0 || drw_ref >= 0) {
+  if (need1 || need2) {
     const int64_t nv8 = (V + 7) / 8;
-    const int64_t vpw = (nv8 + kSW - 1) / kSW;
-    const int64_t w0 = (int64_t)wid * vpw < nv8 ? (int64_t)wid * vpw : nv8;
-    const int64_t w1 = w0 + vpw < nv8 ? w0 + vpw : nv8;
-    // 8-bit masks of the members of vector vi for h1 (low byte) and h2
-    auto match = [&](int64_t vi) __attribute__((always_inline)) -> uint32_t {
-      uint32_t hv[8];
-      const int64_t e0 = vi * 8;
-      if (e0 + 8 <= V) {
-        const u32x4 r = *reinterpret_cast<const u32x4*>(row + e0);
-        const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) hv[j] = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) hv[j] = e0 + j < V ? (uint32_t)row[e0 + j] : 0x10001u;
-      }
+    const int64_t span = (((nv8 + kSB - 1) / kSB) + 7) & ~(int64_t)7;
+    const int64_t t0 = (int64_t)tid * span < nv8 ? (int64_t)tid * span : nv8;
+    const int64_t t1 = t0 + span < nv8 ? t0 + span : nv8;
+    // members of the two items among 8 tokens (bit patterns hv) from e0
+    auto members = [&](const uint32_t (&hv)[8], int64_t e0) __attribute__((always_inline)) -> uint32_t {
+      uint32_t ok = 0xFFu;
+      if (kMask) ok = (mrow[e0 >> 5] >> (e0 & 31)) & 0xFFu;
+      const uint32_t pn = use_pen ? (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu : 0u;
       uint32_t m1 = 0, m2 = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        m1 |= (hv[j] == h1 ? 1u : 0u) << j;
-        m2 |= (hv[j] == h2 ? 1u : 0u) << j;
+        const bool pj = (pn >> j) & 1u;
+        m1 |= (hv[j] == (pj ? hp1 : hu1) ? 1u : 0u) << j;
+        m2 |= (hv[j] == (pj ? hp2 : hu2) ? 1u : 0u) << j;
       }
-      uint32_t ok = 0xFFu;
-      if (kMask) ok &= (mrow[e0 >> 5] >> (e0 & 31)) & 0xFFu;
-      if (use_pen) ok &= ~(sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu;
       return (m1 & ok) | ((m2 & ok) << 8);
     };
+    auto members_at = [&](int64_t vi) __attribute__((always_inline)) -> uint32_t {
+      const int64_t e0 = vi * 8;
+      uint32_t hv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) hv[j] = e0 + j < V ? (uint32_t)row[e0 + j] : 0x10001u;
+      return members(hv, e0);
+    };
+    auto words = [](const u32x4& r, uint32_t (&hv)[8]) __attribute__((always_inline)) {
+      const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) hv[j] = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
+    };
+    const int64_t vlast = t1 < nvec ? t1 : nvec;  // full vectors of the range end here
     uint32_t c1 = 0, c2 = 0;
-    for (int64_t vi = w0 + lane; vi < w1; vi += kWave) {
-      const uint32_t mm = match(vi);
+    for (int64_t s = t0; s < vlast; s += 8) {
+      u32x4 buf[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t vi = s + i < vlast ? s + i : vlast - 1;
+        buf[i] = *reinterpret_cast<const u32x4*>(row + vi * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (s + i < vlast) {
+          uint32_t hv[8];
+          words(buf[i], hv);
+          const uint32_t mm = members(hv, (s + i) * 8);
+          c1 += (uint32_t)__builtin_popcount(mm & 0xFFu);
+          c2 += (uint32_t)__builtin_popcount(mm >> 8);
+          if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)((s + i) * 8 + __builtin_ctz(mm & 0xFFu));
+          if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)((s + i) * 8 + __builtin_ctz(mm >> 8));
+        }
+      }
+    }
+    if (t0 <= nvec && nvec < t1) {  // the partial last vector
+      const uint32_t mm = members_at(nvec);
       c1 += (uint32_t)__builtin_popcount(mm & 0xFFu);
       c2 += (uint32_t)__builtin_popcount(mm >> 8);
-      if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)(vi * 8 + __builtin_ctz(mm & 0xFFu));
-      if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)(vi * 8 + __builtin_ctz(mm >> 8));
+      if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)(nvec * 8 + __builtin_ctz(mm & 0xFFu));
+      if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)(nvec * 8 + __builtin_ctz(mm >> 8));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      c1 += (uint32_t)__shfl_xor((int)c1, o, kWave);
-      c2 += (uint32_t)__shfl_xor((int)c2, o, kWave);
-    }
+    // exclusive prefix of the counts in thread order
+    const uint32_t i1 = wave_scan_u32(c1), i2 = wave_scan_u32(c2);
     __syncthreads();
     if (lane == 0) {
-      sm.red_u[wid] = c1;
-      sm.red_v[wid] = c2;
+      sm.red_u[wid] = lane63_u32(i1);
+      sm.red_v[wid] = lane63_u32(i2);
     }
     __syncthreads();
-    uint32_t p1 = 0, p2 = 0;
+    uint32_t p1 = i1 - c1, p2 = i2 - c2;
 #pragma unroll
     for (int w = 0; w < kSW; ++w)
       if (w < wid) {
         p1 += sm.red_u[w];
         p2 += sm.red_v[w];
       }
-    // the waves holding the j-th member walk their range again
-    const bool walk1 = thr_ref >= 0 && !one1 && (uint32_t)thr_j >= p1 && (uint32_t)thr_j < p1 + c1;
-    const bool walk2 = drw_ref >= 0 && !one2 && (uint32_t)drw_j >= p2 && (uint32_t)drw_j < p2 + c2;
-    if (walk1 || walk2) {
-      uint32_t base1 = p1, base2 = p2;
-      for (int64_t v0 = w0; v0 < w1; v0 += kWave) {
-        const int64_t vi = v0 + lane;
-        const uint32_t mm = vi < w1 ? match(vi) : 0u;
-        const uint32_t n1 = walk1 ? (uint32_t)__builtin_popcount(mm & 0xFFu) : 0u;
-        const uint32_t n2 = walk2 ? (uint32_t)__builtin_popcount(mm >> 8) : 0u;
-        uint32_t i1 = n1, i2 = n2;
+    const bool walk1 = need1 && !one1 && (uint32_t)thr_j >= p1 && (uint32_t)thr_j < p1 + c1;
+    const bool walk2 = need2 && !one2 && (uint32_t)drw_j >= p2 && (uint32_t)drw_j < p2 + c2;
+    // the wave holding a walker reads the walker's range, one vector a lane
+    // (a range is at most 64 vectors)
 #pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-          const uint32_t x1 = (uint32_t)__shfl_up((int)i1, o, kWave);
-          const uint32_t x2 = (uint32_t)__shfl_up((int)i2, o, kWave);
-          if (lane >= o) {
-            i1 += x1;
-            i2 += x2;
+    for (int which = 0; which < 2; ++which) {
+      const unsigned long long wk = __ballot(which == 0 ? walk1 : walk2);
+      if (wk) {
+        const int src = __builtin_ctzll(wk);
+        const int64_t r0 = (int64_t)__builtin_amdgcn_readlane((int)t0, src);
+        const int64_t r1 = (int64_t)__builtin_amdgcn_readlane((int)t1, src);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(which == 0 ? p1 : p2), src);
+        const uint32_t jt = (uint32_t)(which == 0 ? thr_j : drw_j);
+        const int64_t vi = r0 + lane;
+        uint32_t mm = 0;
+        if (vi < r1) {
+          if (vi < nvec) {
+            uint32_t hv[8];
+            words(*reinterpret_cast<const u32x4*>(row + vi * 8), hv);
+            mm = members(hv, vi * 8);
+          } else {
+            mm = members_at(vi);
           }
         }
-        const uint32_t e1 = base1 + i1 - n1, e2 = base2 + i2 - n2;
-        if (walk1 && (uint32_t)thr_j >= e1 && (uint32_t)thr_j < e1 + n1)
-          sm.id_out[0] = (int32_t)(vi * 8 + nth_bit(mm & 0xFFu, (uint32_t)thr_j - e1));
-        if (walk2 && (uint32_t)drw_j >= e2 && (uint32_t)drw_j < e2 + n2)
-          sm.id_out[1] = (int32_t)(vi * 8 + nth_bit(mm >> 8, (uint32_t)drw_j - e2));
-        base1 += (uint32_t)__shfl((int)i1, kWave - 1, kWave);
-        base2 += (uint32_t)__shfl((int)i2, kWave - 1, kWave);
+        const uint32_t mine = which == 0 ? (mm & 0xFFu) : (mm >> 8);
+        const uint32_t n = (uint32_t)__builtin_popcount(mine);
+        const uint32_t ex = base + wave_scan_u32(n) - n;
+        if (n && jt >= ex && jt < ex + n)
+          sm.id_out[which] = (int32_t)(vi * 8 + nth_bit(mine, jt - ex));
       }
     }
   }
   __syncthreads();
+  const int32_t id_thr = sm.id_out[0], id_draw = sm.id_out[1];
+  if (id_thr < 0 || id_draw < 0) return false;  // not reached: every item has its tokens
   if (tid == 0) {
-    const int32_t id_thr = sm.id_out[0], id_draw = sm.id_out[1];
-    const float y_thr = thr_ref >= 0 ? ybin(thr_ref)
-                                     : yproc(sm.sx[-1 - thr_ref], sm.sid[-1 - thr_ref] >> 31);
-    const float x_draw = drw_ref >= 0 ? u2f(hbin_bits(drw_ref) << 16) : sm.sx[-1 - drw_ref];
+    float y_thr;
+    if (thr_ref >= kHBins) {
+      y_thr = ypbin(thr_ref - kHBins);
+    } else if (thr_ref >= 0) {
+      y_thr = ybin(thr_ref);
+    } else {
+      const uint32_t s = (uint32_t)(-1 - thr_ref);
+      y_thr = is_pen(sm.sid[s]) ? ypen(sm.sx[s]) : sm.sx[s] / Tc + 0.0f;
+    }
+    const float x_draw = u2f((uint32_t)row[id_draw] << 16);
     const float slp = (float)::log((double)w_draw / (double)Wp);
     write_row(a, b, GTP_ROW_OK, id_draw, x_draw - lse_raw, slp, (int32_t)R, y_thr, id_thr);
   }
@@ -1533,8 +1803,9 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   // normal y = x / T)
   const bool aligned = (reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0 &&
                        ((a.row_stride * 2) & 15) == 0;
-  const bool use_pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
-  if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f && !use_pen) {
+  // (penalised counts are 16-bit: at most 65535 history entries)
+  if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&
+      a.hist_len <= 65535) {
     if (a.mask)
       hipLaunchKernelGGL((sampler_hist_kernel<uint16_t, true>), grid, block, 0, s, a);
     else
