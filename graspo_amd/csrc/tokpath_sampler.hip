@@ -923,11 +923,11 @@ __global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
 constexpr int kHBins = 16384;
 constexpr uint32_t kHELo = 87;
 constexpr int kHSegBins = kHBins / kSB;  // 16 bins per thread and per segment
-constexpr int kHSCap = 1024;             // singletons of a row
+constexpr int kHSCap = 512;              // singletons of a row
 constexpr int kHXCap = 64;               // extra items of one resolved segment
 constexpr int kHItems = kHSegBins + kHXCap;
 constexpr int kHPenSpan = 2048;          // penalised-value bins one segment may span
-constexpr int kHG = 4;                   // vectors per thread per stream step
+constexpr int kHG = 2;                   // vectors per thread per stream step
 constexpr uint32_t kNoPattern = 0x10000u;  // matches no 16-bit pattern
 
 struct alignas(16) HistSmem {
@@ -939,6 +939,8 @@ struct alignas(16) HistSmem {
   uint16_t sbin[kHSCap];                 // largest bin whose y <= the singleton's y (0xFFFF: none)
   unsigned long long segw[kSB];          // weight of the extra items of each segment
   uint32_t segc[kSB];
+  uint32_t seg_plo[kSB];                 // penalised bins placed in each segment: [plo, phi)
+  uint32_t seg_phi[kSB];
   // the resolved segment (wave 0)
   unsigned long long it_w[kHItems];      // per-token weight of each item, in rank order
   uint32_t it_c[kHItems];                // tokens in the item
@@ -946,6 +948,8 @@ struct alignas(16) HistSmem {
   int32_t it_aux[kHItems];               // penalised bin merged into bin b, or -1
   uint32_t xcode[kHXCap];                // extra items: kHBins + p, or singleton slot
   int32_t aux_q[kHSegBins];
+  float rys[kHSegBins];                  // y and unpenalised count of its bins
+  uint32_t rcs[kHSegBins];
   float red3[kSW][3];
   uint32_t red_u[kSW];
   uint32_t red_v[kSW];
@@ -1062,10 +1066,15 @@ __device__ __forceinline__ unsigned long long wave_sort_desc_u64(unsigned long l
   return v;
 }
 
-// One row; false when the row needs the row-wise path instead.
+// One row; false when the row needs the row-wise path instead.  Without a
+// mask every token is counted in the bins or kept as a singleton, so the
+// raw log-sum-exp comes from the counts (one exp per distinct value) and
+// the stream does no floating-point work; with a mask the stream folds it
+// token by token.
 template <typename T, bool kMask>
 __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSmem& sm) {
   static_assert(sizeof(T) == 2, "bf16 rows only");
+  constexpr bool kLseStream = kMask;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const T* __restrict__ row = reinterpret_cast<const T*>(a.logits) + b * a.row_stride;
   const uint32_t* __restrict__ mrow = kMask ? a.mask + b * a.mask_stride : nullptr;
@@ -1074,16 +1083,15 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   const float Tc = a.T > 1e-6f ? a.T : 1e-6f;
   const float rho = a.rho;
   const float u = a.uniforms[b];
-  auto ybin = [&](int bn) __attribute__((always_inline)) -> float {
-    return u2f(hbin_bits(bn) << 16) / Tc + 0.0f;
+  auto xbin = [&](int bn) __attribute__((always_inline)) -> float {
+    return u2f(hbin_bits(bn) << 16);
   };
+  auto ybin = [&](int bn) __attribute__((always_inline)) -> float { return xbin(bn) / Tc + 0.0f; };
   auto ypen = [&](float x) __attribute__((always_inline)) -> float {
     const float xp = x < 0.0f ? x * rho : x / rho;
     return xp / Tc + 0.0f;
   };
-  auto ypbin = [&](int p) __attribute__((always_inline)) -> float {
-    return ypen(u2f(hbin_bits(p) << 16));
-  };
+  auto ypbin = [&](int p) __attribute__((always_inline)) -> float { return ypen(xbin(p)); };
   auto is_pen = [&](int64_t id) __attribute__((always_inline)) -> bool {
     return use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
   };
@@ -1119,6 +1127,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     for (int i = tid; i < (int)((V + 31) / 32); i += kSB) sm.pen[i] = 0u;
   sm.segw[tid] = 0ull;
   sm.segc[tid] = 0u;
+  sm.seg_plo[tid] = 0xFFFFu;
+  sm.seg_phi[tid] = 0u;
   if (tid < kHSegBins) sm.aux_q[tid] = -1;
   if (tid == 0) {
     sm.ns = 0u;
@@ -1127,7 +1137,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   }
   __syncthreads();
 
-  // ---- 1. stream: raw log-sum-exp, value counts, singletons
+  // ---- 1. stream: value counts, singletons (and with a mask the raw
+  // log-sum-exp)
   Lse3 st{kNegInf, 0.0f, 0.0f};
   auto single = [&](int64_t id, float x) __attribute__((always_inline)) {
     const uint32_t slot = atomicAdd(&sm.ns, 1u);
@@ -1138,23 +1149,25 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   };
   auto fold = [&](float(&x)[kHG][8], const u32x4(&raw)[kHG], uint32_t sw, int64_t vbase,
                   bool last) __attribute__((always_inline)) {
-    float gm[kHG];
+    if (kLseStream) {
+      float gm[kHG];
 #pragma unroll
-    for (int k = 0; k < kHG; ++k) gm[k] = vec_max<8>(x[k]);
-    if (last) {
+      for (int k = 0; k < kHG; ++k) gm[k] = vec_max<8>(x[k]);
+      if (last) {
 #pragma unroll
-      for (int k = 0; k < kHG; ++k)
-        if (vbase + (int64_t)k * kWave >= nvec) {
-          gm[k] = kNegInf;
+        for (int k = 0; k < kHG; ++k)
+          if (vbase + (int64_t)k * kWave >= nvec) {
+            gm[k] = kNegInf;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) x[k][j] = kNegInf;
-        }
+            for (int j = 0; j < 8; ++j) x[k][j] = kNegInf;
+          }
+      }
+      float cm = gm[0];
+#pragma unroll
+      for (int k = 1; k + 1 < kHG; k += 2) cm = max3raw(cm, gm[k], gm[k + 1]);
+      if (!(kHG & 1)) cm = max3raw(cm, gm[kHG - 1], gm[kHG - 1]);
+      lse_fold_block_max<false, kHG, 8>(st, x, cm);
     }
-    float cm = gm[0];
-#pragma unroll
-    for (int k = 1; k + 1 < kHG; k += 2) cm = max3raw(cm, gm[k], gm[k + 1]);
-    if (!(kHG & 1)) cm = max3raw(cm, gm[kHG - 1], gm[kHG - 1]);
-    lse_fold_block_max<false, kHG, 8>(st, x, cm);
 #pragma unroll
     for (int k = 0; k < kHG; ++k) {
       const int64_t vi = vbase + (int64_t)k * kWave;
@@ -1168,12 +1181,20 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       uint32_t sg = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint32_t h = (j & 1) ? (wds[j >> 1] >> 16) : (wds[j >> 1] & 0xFFFFu);
-        const int bn = hbin_of(h);
+        // bin = 2^13 + (idx ^ sign): 2^13 + idx for x > 0, 2^13 - 1 - idx for x < 0
+        const uint32_t w = wds[j >> 1];
+        const uint32_t h = (j & 1) ? w >> 16 : w & 0xFFFFu;
+        const uint32_t mag = h & 0x7FFFu;
+        const uint32_t sgn = (j & 1) ? (uint32_t)((int32_t)w >> 31)
+                                     : (uint32_t)((int32_t)(w << 16) >> 31);
+        const uint32_t idx = mag - (kHELo << 7);
+        const bool in = idx < 64u * 128u;
         const bool ok = (ab >> j) & 1u;
         // tokens outside the bins and masked tokens count in the lane's spill word
-        atomicAdd(&sm.cnt[ok && bn >= 0 ? bn : kHBins + lane], 1u);
-        sg |= (ok && bn < 0 && ((h >> 7) & 0xFFu) != 0xFFu) ? (1u << j) : 0u;
+        atomicAdd(&sm.cnt[in && ok ? (idx ^ sgn) + kHBins / 2 : kHBins + lane], 1u);
+        // kept one by one: allowed tokens outside the bins except -inf
+        // (NaN and +inf among them make the row non-finite)
+        sg |= (ok && !in && h != 0xFF80u) ? (1u << j) : 0u;
       }
       if (sg) {
 #pragma unroll
@@ -1185,20 +1206,24 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   stream_chunks<T, kHG, false, kMask>(row, 0, nvec, mrow, &sm.chunk_ctr, fold);
   for (int64_t id = nvec * 8 + tid; id < V; id += kSB) {
     const float xv = Elem<T>::get(row, id);
-    float x1[1][4] = {{xv, kNegInf, kNegInf, kNegInf}};
-    lse_fold_block_max<false, 1, 4>(st, x1, xv);
+    if (kLseStream) {
+      float x1[1][4] = {{xv, kNegInf, kNegInf, kNegInf}};
+      lse_fold_block_max<false, 1, 4>(st, x1, xv);
+    }
     if (allowed(id)) {
       const uint32_t h = f2u(xv) >> 16;
       const int bn = hbin_of(h);
       if (bn >= 0)
         atomicAdd(&sm.cnt[bn], 1u);
-      else if (((h >> 7) & 0xFFu) != 0xFFu)
+      else if (h != 0xFF80u)
         single(id, xv);
     }
   }
   float lm = st.m, ls = st.s;
-  block_lse2<kSB>(lm, ls, sm.red3);  // its barrier completes the counts and singletons
-  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+  if (kLseStream)
+    block_lse2<kSB>(lm, ls, sm.red3);  // its barrier completes the counts and singletons
+  else
+    __syncthreads();
 
   // ---- history: each distinct, allowed penalised id moves to the
   // penalised count of its value (singletons read the bitmap later)
@@ -1223,21 +1248,11 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     }
   }
   bad_hist = __syncthreads_or(bad_hist);
-  int32_t status = GTP_ROW_OK;
-  if (ls != ls || lm == kPosInf)
-    status = GTP_ROW_NONFINITE;
-  else if (bad_hist)
-    status = GTP_ROW_BAD_HISTORY;
-  else if (!(u >= 0.0f && u < 1.0f))
-    status = GTP_ROW_BAD_UNIFORM;
-  if (status != GTP_ROW_OK) {
-    if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
-    return true;
-  }
   const uint32_t ns = sm.ns;
-  if (ns > (uint32_t)kHSCap) return false;
+  if (!kLseStream && ns > (uint32_t)kHSCap) return false;  // the count-based sum needs them all
 
-  // ---- 2. m, per-segment count and weight, extra items placed
+  // ---- 2. this thread's 16 bins (segment tid): counts, raw log-sum-exp
+  // terms (without a mask), largest processed logit
   const int seg0 = tid * kHSegBins;
   uint32_t cu[kHSegBins], cp[kHSegBins];
   {
@@ -1262,23 +1277,65 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       }
     }
   }
+  if (!kLseStream) {
+    // raw counts per value: unpenalised + penalised
+    int top = -1;
+#pragma unroll
+    for (int q = 0; q < kHSegBins; ++q)
+      if (cu[q] + cp[q]) top = q;
+    float mt = top >= 0 ? xbin(seg0 + top) : kNegInf;
+    for (uint32_t s = tid; s < ns; s += kSB) mt = fmaxf(mt, sm.sx[s]);
+    float mw = mt;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o, kWave));
+    // terms against the wave maximum (exact enough: one rescale per wave)
+    // (a NaN singleton makes the sum NaN, an infinite one too)
+    float sacc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kHSegBins; ++q) {
+      const uint32_t c = cu[q] + cp[q];
+      if (c) sacc += (float)c * __builtin_amdgcn_exp2f((xbin(seg0 + q) - mw) * kLog2e);
+    }
+    for (uint32_t s = tid; s < ns; s += kSB)
+      sacc += __builtin_amdgcn_exp2f((sm.sx[s] - mw) * kLog2e);
+    lm = mw;
+    ls = sacc;
+    block_lse2<kSB>(lm, ls, sm.red3);
+  }
+  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+  int32_t status = GTP_ROW_OK;
+  if (ls != ls || lm == kPosInf)
+    status = GTP_ROW_NONFINITE;
+  else if (bad_hist)
+    status = GTP_ROW_BAD_HISTORY;
+  else if (!(u >= 0.0f && u < 1.0f))
+    status = GTP_ROW_BAD_UNIFORM;
+  if (status != GTP_ROW_OK) {
+    if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
+    return true;
+  }
+  if (ns > (uint32_t)kHSCap) return false;
+
   uint32_t C_t = 0;
-  int top_u = -1;
-  float ypq[kHSegBins];
-  bool odd = false;
-  float ymax = kNegInf;
+  int top_u = -1, lo_p = -1, hi_p = -1;
 #pragma unroll
   for (int q = 0; q < kHSegBins; ++q) {
     C_t += cu[q];
     if (cu[q]) top_u = q;
-    ypq[q] = kNegInf;
     if (cp[q]) {
-      ypq[q] = ypbin(seg0 + q);
-      odd |= !(ypq[q] > kNegInf && ypq[q] < kPosInf);
-      ymax = fmaxf(ymax, ypq[q]);
+      hi_p = q;
+      if (lo_p < 0) lo_p = q;
     }
   }
-  if (top_u >= 0) ymax = fmaxf(ymax, ybin(seg0 + top_u));
+  // y of penalised values is monotone in the value: the range's extremes
+  // bound it (an overflow to +-inf shows there)
+  float ymax = top_u >= 0 ? ybin(seg0 + top_u) : kNegInf;
+  bool odd = false;
+  if (hi_p >= 0) {
+    const float yh = ypbin(seg0 + hi_p), yl = ypbin(seg0 + lo_p);
+    odd = !(yh < kPosInf && yl > kNegInf);
+    ymax = fmaxf(ymax, yh);
+  }
   for (uint32_t s = tid; s < ns; s += kSB) {
     const float x = sm.sx[s];
     const float y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
@@ -1291,24 +1348,40 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
 #pragma unroll
   for (int q = 0; q < kHSegBins; ++q)
     if (cu[q]) W_t += (unsigned long long)cu[q] * detexp_fix(ybin(seg0 + q) - m);
-#pragma unroll
-  for (int q = 0; q < kHSegBins; ++q) {
-    if (cp[q]) {
-      const float y = ypq[q];
+  // extra items (this thread's penalised values, then its singletons) join
+  // the segment of the largest bin at or below their y; a segment records
+  // the range of penalised values it received
+  {
+    const uint32_t n_own = ns > (uint32_t)tid ? (ns - (uint32_t)tid + kSB - 1) / kSB : 0u;
+    const uint32_t first = lo_p >= 0 ? (uint32_t)lo_p : (uint32_t)kHSegBins;
+    const uint32_t last_p = hi_p >= 0 ? (uint32_t)hi_p + 1u : 0u;
+#pragma unroll 1
+    for (uint32_t i = first; i < (uint32_t)kHSegBins + n_own; ++i) {
+      if (i >= last_p && i < (uint32_t)kHSegBins) continue;
+      float y;
+      uint32_t c;
+      uint32_t s = 0xFFFFFFFFu;
+      if (i < (uint32_t)kHSegBins) {
+        c = pcnt_of(sm, seg0 + (int)i);
+        if (!c) continue;
+        y = ypbin(seg0 + (int)i);
+      } else {
+        s = (uint32_t)tid + (i - kHSegBins) * kSB;
+        c = 1u;
+        const float x = sm.sx[s];
+        y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
+      }
       const int bf = place(y);
       const int sg = bf < 0 ? 0 : bf / kHSegBins;
-      atomicAdd(&sm.segw[sg], (unsigned long long)cp[q] * detexp_fix(y - m));
-      atomicAdd(&sm.segc[sg], cp[q]);
+      if (s != 0xFFFFFFFFu) {
+        sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
+      } else {
+        atomicMin(&sm.seg_plo[sg], (uint32_t)(seg0 + (int)i));
+        atomicMax(&sm.seg_phi[sg], (uint32_t)(seg0 + (int)i) + 1u);
+      }
+      atomicAdd(&sm.segw[sg], (unsigned long long)c * detexp_fix(y - m));
+      atomicAdd(&sm.segc[sg], c);
     }
-  }
-  for (uint32_t s = tid; s < ns; s += kSB) {
-    const float x = sm.sx[s];
-    const float y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
-    const int bf = place(y);
-    sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
-    const int sg = bf < 0 ? 0 : bf / kHSegBins;
-    atomicAdd(&sm.segw[sg], detexp_fix(y - m));
-    atomicAdd(&sm.segc[sg], 1u);
   }
   __syncthreads();
   W_t += sm.segw[tid];
@@ -1370,8 +1443,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     __syncthreads();
     if (wid == 0) {
       const int b0 = t * kHSegBins;
-      bool bad = false;
-      // the segment's bins, as scalars
+      // the segment's bins, in scalar registers
       float ys[kHSegBins];
       uint32_t cs[kHSegBins];
       {
@@ -1383,50 +1455,15 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
           cs[q] = (uint32_t)__builtin_amdgcn_readlane((int)cl, q);
         }
       }
-      // penalised values placed here: [plo, phi), found by bisection
-      int plo = 0, phi = 0;
-      if (use_pen) {
-        int r = 0;
-        if (lane < 2) {
-          if (lane == 0 && t == 0) {
-            r = 0;
-          } else if (lane == 1 && t == kSB - 1) {
-            r = kHBins;
-          } else {
-            const float yt = ybin(b0 + kHSegBins * lane);
-            int lo = 0, hi = kHBins;
-            while (lo < hi) {
-              const int mid = (lo + hi) >> 1;
-              if (ypbin(mid) >= yt)
-                hi = mid;
-              else
-                lo = mid + 1;
-            }
-            r = lo;
-          }
-        }
-        plo = __builtin_amdgcn_readlane(r, 0);
-        phi = __builtin_amdgcn_readlane(r, 1);
-        if (phi - plo > kHPenSpan) bad = true;
-      }
-      // extra items: penalised values not equal to a bin with tokens, and
-      // the segment's singletons
+      const int plo = (int)sm.seg_plo[t], phi = (int)sm.seg_phi[t];
+      bool bad = phi - plo > kHPenSpan;
+      // extra items: the penalised values placed here, and the segment's
+      // singletons
       uint32_t k = 0;
       if (!bad) {
         for (int base = plo; base < phi; base += kWave) {
           const int p = base + lane;
-          bool ext = false;
-          if (p < phi && pcnt_of(sm, p)) {
-            const float y = ypbin(p);
-            int tq = -1;
-#pragma unroll
-            for (int q = 0; q < kHSegBins; ++q)
-              if (cs[q] && ys[q] == y) tq = q;
-            if (tq >= 0)
-              sm.aux_q[tq] = p;
-            else
-              ext = true;
-          }
+          const bool ext = p < phi && pcnt_of(sm, p) != 0u;
           const unsigned long long mk = __ballot(ext);
           const uint32_t pos = k + (uint32_t)__builtin_popcountll(mk & ((1ull << lane) - 1ull));
           if (ext && pos < (uint32_t)kHXCap) sm.xcode[pos] = (uint32_t)(kHBins + p);
@@ -1446,6 +1483,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         }
         bad = k > (uint32_t)kHXCap;
       }
+      wave_lds_sync();
       // extras sorted by rank: key = (ord y, ~tag), tag = id << 12 | slot for
       // a singleton, 2^30 | p for a penalised value
       const bool have = !bad && (uint32_t)lane < k;
@@ -1466,31 +1504,43 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         }
         key = ((unsigned long long)ord32(y) << 32) | (unsigned long long)(0xFFFFFFFFu - tag);
       }
-      wave_lds_sync();  // xcode and aux_q, written above, are read below
       if (k > 1u && !bad) key = wave_sort_desc_u64(key);
       const uint32_t tag_me = 0xFFFFFFFFu - (uint32_t)key;
       const uint32_t oy_me = (uint32_t)(key >> 32);
       const float y_me = have ? unord32(oy_me) : kNegInf;
       const bool pen_item = have && (tag_me & 0x40000000u);
-      // ties that the item order cannot express
+      // a penalised value equal to a bin with tokens merges into it; other
+      // equalities the item order cannot express leave this path
+      int merge_q = -1;
+      uint32_t nb_above = 0;
+      bool tie = false;
+#pragma unroll
+      for (int q = 0; q < kHSegBins; ++q) {
+        if (cs[q]) {
+          nb_above += ys[q] > y_me ? 1u : 0u;
+          if (have && ys[q] == y_me) {
+            if (pen_item)
+              merge_q = q;
+            else
+              tie = true;
+          }
+        }
+      }
       {
         const uint32_t oy_next = (uint32_t)__shfl_down((int)oy_me, 1, kWave);
         const bool pen_next = __shfl_down((int)pen_item, 1, kWave) != 0;
-        bool tie = have && (uint32_t)lane + 1u < k && oy_next == oy_me && (pen_item || pen_next);
-        if (have && !pen_item) {
-#pragma unroll
-          for (int q = 0; q < kHSegBins; ++q)
-            if (cs[q] && ys[q] == y_me) tie = true;
-        }
-        bad |= __ballot(tie) != 0ull;
+        tie |= have && (uint32_t)lane + 1u < k && oy_next == oy_me && (pen_item || pen_next);
       }
+      bad |= __ballot(tie) != 0ull;
+      const unsigned long long merged = __ballot(merge_q >= 0);
+      const bool own = have && merge_q < 0;  // an item of its own
+      const uint32_t rank_me =
+          (uint32_t)__builtin_popcountll(__ballot(own) & ((1ull << lane) - 1ull));
+      const uint32_t n_own_x = (uint32_t)__builtin_popcountll(__ballot(own));
       if (!bad) {
-        if (have) {
-          uint32_t nb_above = 0;
-#pragma unroll
-          for (int q = 0; q < kHSegBins; ++q)
-            if (cs[q] && ys[q] > y_me) ++nb_above;
-          const uint32_t pos = (uint32_t)lane + nb_above;
+        if (merge_q >= 0) sm.aux_q[merge_q] = (int32_t)(tag_me & 0x3FFFFu);
+        if (own) {
+          const uint32_t pos = rank_me + nb_above;
           sm.it_w[pos] = detexp_fix(y_me - m);
           if (pen_item) {
             const int p = (int)(tag_me & 0x3FFFFu);
@@ -1502,14 +1552,15 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
           }
           sm.it_aux[pos] = -1;
         }
+        wave_lds_sync();
         uint32_t nzb = 0;
 #pragma unroll
         for (int q = kHSegBins - 1; q >= 0; --q) {
-          const unsigned long long above_x = __ballot(have && y_me > ys[q]);
           if (cs[q]) {
+            const unsigned long long above_x = __ballot(own && y_me > ys[q]);
             if (lane == 0) {
               const uint32_t pos = nzb + (uint32_t)__builtin_popcountll(above_x);
-              const int32_t ax = sm.aux_q[q];
+              const int32_t ax = merged ? sm.aux_q[q] : -1;
               sm.it_w[pos] = detexp_fix(ys[q] - m);
               sm.it_c[pos] = cs[q] + (ax >= 0 ? pcnt_of(sm, ax) : 0u);
               sm.it_ref[pos] = b0 + q;
@@ -1519,7 +1570,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
           }
         }
         wave_lds_sync();
-        const uint32_t n_it = nzb + k;
+        const uint32_t n_it = nzb + n_own_x;
         uint32_t c2[2] = {0u, 0u};
         unsigned long long w2[2] = {0ull, 0ull}, wt2[2] = {0ull, 0ull};
 #pragma unroll
@@ -1626,8 +1677,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   // order, among the allowed tokens with the item's bit pattern (unpenalised
   // for a bin, penalised for a penalised value; both for a merged bin).
   // Thread t scans a contiguous range of vectors; a one-token item takes the
-  // first match, else per-thread counts pick the thread that walks its
-  // range again to the j-th match.
+  // first match, else per-thread counts pick the thread whose range the
+  // walker's wave reads again, one vector a lane.
   uint32_t hu1 = kNoPattern, hp1 = kNoPattern, hu2 = kNoPattern, hp2 = kNoPattern;
   if (thr_ref >= kHBins) {
     hp1 = hbin_bits(thr_ref - kHBins);
@@ -1643,6 +1694,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   }
   const bool need1 = thr_ref >= 0, need2 = drw_ref >= 0;
   const bool one1 = need1 && thr_c == 1u, one2 = need2 && drw_c == 1u;
+  const bool any_pp = hp1 != kNoPattern || hp2 != kNoPattern;  // a penalised pattern to match
   __syncthreads();
   if (tid == 0) {
     sm.id_out[0] = need1 ? -1 : (int32_t)sm.sid[-1 - thr_ref];
@@ -1653,17 +1705,33 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     const int64_t span = (((nv8 + kSB - 1) / kSB) + 7) & ~(int64_t)7;
     const int64_t t0 = (int64_t)tid * span < nv8 ? (int64_t)tid * span : nv8;
     const int64_t t1 = t0 + span < nv8 ? t0 + span : nv8;
-    // members of the two items among 8 tokens (bit patterns hv) from e0
+    // members of the two items among the 8 tokens (bit patterns hv) from e0:
+    // low byte item 1, high byte item 2
     auto members = [&](const uint32_t (&hv)[8], int64_t e0) __attribute__((always_inline)) -> uint32_t {
       uint32_t ok = 0xFFu;
       if (kMask) ok = (mrow[e0 >> 5] >> (e0 & 31)) & 0xFFu;
-      const uint32_t pn = use_pen ? (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu : 0u;
       uint32_t m1 = 0, m2 = 0;
+      if (any_pp) {
+        const uint32_t pn = use_pen ? (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu : 0u;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool pj = (pn >> j) & 1u;
-        m1 |= (hv[j] == (pj ? hp1 : hu1) ? 1u : 0u) << j;
-        m2 |= (hv[j] == (pj ? hp2 : hu2) ? 1u : 0u) << j;
+        for (int j = 0; j < 8; ++j) {
+          const bool pj = (pn >> j) & 1u;
+          m1 |= (hv[j] == (pj ? hp1 : hu1) ? 1u : 0u) << j;
+          m2 |= (hv[j] == (pj ? hp2 : hu2) ? 1u : 0u) << j;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          m1 |= (hv[j] == hu1 ? 1u : 0u) << j;
+          m2 |= (hv[j] == hu2 ? 1u : 0u) << j;
+        }
+        if (use_pen) {
+          const uint32_t pn = (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu;
+          if ((m1 | m2) & pn) {
+            m1 &= ~pn;
+            m2 &= ~pn;
+          }
+        }
       }
       return (m1 & ok) | ((m2 & ok) << 8);
     };
@@ -1681,15 +1749,16 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     };
     const int64_t vlast = t1 < nvec ? t1 : nvec;  // full vectors of the range end here
     uint32_t c1 = 0, c2 = 0;
-    for (int64_t s = t0; s < vlast; s += 8) {
-      u32x4 buf[8];
+#pragma unroll 1
+    for (int64_t s = t0; s < vlast; s += 4) {
+      u32x4 buf[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
         const int64_t vi = s + i < vlast ? s + i : vlast - 1;
         buf[i] = *reinterpret_cast<const u32x4*>(row + vi * 8);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
         if (s + i < vlast) {
           uint32_t hv[8];
           words(buf[i], hv);
