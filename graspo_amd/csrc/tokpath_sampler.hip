@@ -1049,6 +1049,57 @@ __device__ __forceinline__ uint32_t lane63_u32(uint32_t v) {
 __device__ __forceinline__ unsigned long long lane63_u64(unsigned long long v) {
   return ((unsigned long long)lane63_u32((uint32_t)(v >> 32)) << 32) | lane63_u32((uint32_t)v);
 }
+// Sums within each row of 16 lanes (inclusive; lane 15 of a row holds the
+// row's total).
+__device__ __forceinline__ uint32_t row_scan_u32(uint32_t x) {
+  x += dpp_take<0x111, 0xF>(x);
+  x += dpp_take<0x112, 0xF>(x);
+  x += dpp_take<0x114, 0xF>(x);
+  x += dpp_take<0x118, 0xF>(x);
+  return x;
+}
+__device__ __forceinline__ unsigned long long row_scan_u64(unsigned long long x) {
+#define GTP_ROW64_STEP(ctrl)                                                         \
+  {                                                                                  \
+    const uint32_t lo = dpp_take<ctrl, 0xF>((uint32_t)x);                            \
+    const uint32_t hi = dpp_take<ctrl, 0xF>((uint32_t)(x >> 32));                    \
+    x += ((unsigned long long)hi << 32) | lo;                                        \
+  }
+  GTP_ROW64_STEP(0x111)
+  GTP_ROW64_STEP(0x112)
+  GTP_ROW64_STEP(0x114)
+  GTP_ROW64_STEP(0x118)
+#undef GTP_ROW64_STEP
+  return x;
+}
+// Wave maximum of a float (every lane gets it); NaN inputs are ignored.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_take_max(float v) {
+  return u2f((uint32_t)__builtin_amdgcn_update_dpp((int)0xFF800000u, (int)f2u(v), kCtrl, kRowMask,
+                                                   0xF, false));
+}
+__device__ __forceinline__ float wave_max_f(float x) {
+  x = fmaxf(x, dpp_take_max<0x111, 0xF>(x));
+  x = fmaxf(x, dpp_take_max<0x112, 0xF>(x));
+  x = fmaxf(x, dpp_take_max<0x114, 0xF>(x));
+  x = fmaxf(x, dpp_take_max<0x118, 0xF>(x));
+  x = fmaxf(x, dpp_take_max<0x142, 0xA>(x));
+  x = fmaxf(x, dpp_take_max<0x143, 0xC>(x));
+  return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(x), kWave - 1));
+}
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_take_f(float v) {
+  return u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), kCtrl, kRowMask, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+  x += dpp_take_f<0x111, 0xF>(x);
+  x += dpp_take_f<0x112, 0xF>(x);
+  x += dpp_take_f<0x114, 0xF>(x);
+  x += dpp_take_f<0x118, 0xF>(x);
+  x += dpp_take_f<0x142, 0xA>(x);
+  x += dpp_take_f<0x143, 0xC>(x);
+  return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(x), kWave - 1));
+}
 
 // wave sort of 64-bit keys, descending (one per lane)
 __device__ __forceinline__ unsigned long long wave_sort_desc_u64(unsigned long long v) {
@@ -1251,56 +1302,62 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   const uint32_t ns = sm.ns;
   if (!kLseStream && ns > (uint32_t)kHSCap) return false;  // the count-based sum needs them all
 
-  // ---- 2. this thread's 16 bins (segment tid): counts, raw log-sum-exp
-  // terms (without a mask), largest processed logit
-  const int seg0 = tid * kHSegBins;
-  uint32_t cu[kHSegBins], cp[kHSegBins];
-  {
-    const u32x4* c4 = reinterpret_cast<const u32x4*>(sm.cnt + seg0);
-    const u32x4* p4 = reinterpret_cast<const u32x4*>(sm.pcnt2 + seg0 / 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 v = c4[i];
-      cu[4 * i] = v.x;
-      cu[4 * i + 1] = v.y;
-      cu[4 * i + 2] = v.z;
-      cu[4 * i + 3] = v.w;
+  // ---- 2. the bins, in blocks of 64 values: wave w takes blocks w, w + 16,
+  // ... (so dense value ranges spread over all waves) and skips empty
+  // blocks; a row of 16 lanes covers one segment.
+  // Pass A: raw log-sum-exp terms from the counts (without a mask), each
+  // segment's unpenalised count, the lane's highest bins with tokens.
+  float lm_l = kNegInf, ls_l = 0.0f;
+  int top_u = -1, lo_p = -1, hi_p = -1;
+#pragma unroll 1
+  for (int kb = 0; kb < kHBins / kSB; ++kb) {
+    const int bb = kb * kSB + wid * kWave + lane;
+    const uint32_t c = sm.cnt[bb], pc = pcnt_of(sm, bb);
+    if (__ballot((c | pc) != 0u) == 0ull) continue;
+    if (c) top_u = bb;
+    if (pc) {
+      hi_p = bb;
+      if (lo_p < 0) lo_p = bb;
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const u32x4 v = p4[i];
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        cp[8 * i + 2 * k] = w[k] & 0xFFFFu;
-        cp[8 * i + 2 * k + 1] = w[k] >> 16;
-      }
+    if (!kLseStream && (c | pc)) {  // values rise with kb: each is the lane's new maximum
+      const float x = xbin(bb);
+      ls_l = ls_l * __builtin_amdgcn_exp2f((lm_l - x) * kLog2e) + (float)(c + pc);
+      lm_l = x;
     }
+    const uint32_t rs = row_scan_u32(c);
+    if ((lane & 15) == 15) sm.segc[bb >> 4] = rs;
   }
   if (!kLseStream) {
-    // raw counts per value: unpenalised + penalised
-    int top = -1;
-#pragma unroll
-    for (int q = 0; q < kHSegBins; ++q)
-      if (cu[q] + cp[q]) top = q;
-    float mt = top >= 0 ? xbin(seg0 + top) : kNegInf;
-    for (uint32_t s = tid; s < ns; s += kSB) mt = fmaxf(mt, sm.sx[s]);
-    float mw = mt;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o, kWave));
-    // terms against the wave maximum (exact enough: one rescale per wave)
-    // (a NaN singleton makes the sum NaN, an infinite one too)
-    float sacc = 0.0f;
-#pragma unroll
-    for (int q = 0; q < kHSegBins; ++q) {
-      const uint32_t c = cu[q] + cp[q];
-      if (c) sacc += (float)c * __builtin_amdgcn_exp2f((xbin(seg0 + q) - mw) * kLog2e);
+    // singletons (a NaN one makes the sum NaN, an infinite one the maximum)
+    for (uint32_t s = tid; s < ns; s += kSB) {
+      const float x = sm.sx[s];
+      if (x > lm_l) {
+        ls_l = ls_l * __builtin_amdgcn_exp2f((lm_l - x) * kLog2e) + 1.0f;
+        lm_l = x;
+      } else {
+        ls_l += __builtin_amdgcn_exp2f((x - lm_l) * kLog2e);
+      }
     }
-    for (uint32_t s = tid; s < ns; s += kSB)
-      sacc += __builtin_amdgcn_exp2f((sm.sx[s] - mw) * kLog2e);
-    lm = mw;
-    ls = sacc;
-    block_lse2<kSB>(lm, ls, sm.red3);
+    const float mw = wave_max_f(lm_l);
+    float sw = ls_l * __builtin_amdgcn_exp2f((lm_l - mw) * kLog2e);
+    if (!(lm_l > kNegInf)) sw = ls_l;  // no terms (0), or a NaN sum
+    sw = wave_sum_f(sw);
+    if (lane == 0) {
+      sm.red3[wid][0] = mw;
+      sm.red3[wid][1] = sw;
+    }
+    __syncthreads();
+    float mb = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w) mb = fmaxf(mb, sm.red3[w][0]);
+    float sb = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w) {
+      const float mwv = sm.red3[w][0], swv = sm.red3[w][1];
+      sb += mwv > kNegInf ? swv * __builtin_amdgcn_exp2f((mwv - mb) * kLog2e) : swv;
+    }
+    lm = mb;
+    ls = sb;
   }
   const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
   int32_t status = GTP_ROW_OK;
@@ -1316,23 +1373,12 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   }
   if (ns > (uint32_t)kHSCap) return false;
 
-  uint32_t C_t = 0;
-  int top_u = -1, lo_p = -1, hi_p = -1;
-#pragma unroll
-  for (int q = 0; q < kHSegBins; ++q) {
-    C_t += cu[q];
-    if (cu[q]) top_u = q;
-    if (cp[q]) {
-      hi_p = q;
-      if (lo_p < 0) lo_p = q;
-    }
-  }
-  // y of penalised values is monotone in the value: the range's extremes
-  // bound it (an overflow to +-inf shows there)
-  float ymax = top_u >= 0 ? ybin(seg0 + top_u) : kNegInf;
+  // m = the largest processed logit (y of penalised values is monotone in
+  // the value: a lane's extremes bound it, and show an overflow to +-inf)
+  float ymax = top_u >= 0 ? ybin(top_u) : kNegInf;
   bool odd = false;
   if (hi_p >= 0) {
-    const float yh = ypbin(seg0 + hi_p), yl = ypbin(seg0 + lo_p);
+    const float yh = ypbin(hi_p), yl = ypbin(lo_p);
     odd = !(yh < kPosInf && yl > kNegInf);
     ymax = fmaxf(ymax, yh);
   }
@@ -1342,50 +1388,55 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     odd |= !(y > kNegInf && y < kPosInf);
     ymax = fmaxf(ymax, y);
   }
-  if (__syncthreads_or(odd)) return false;
-  const float m = block_max_hist(sm, ymax);
-  unsigned long long W_t = 0;
-#pragma unroll
-  for (int q = 0; q < kHSegBins; ++q)
-    if (cu[q]) W_t += (unsigned long long)cu[q] * detexp_fix(ybin(seg0 + q) - m);
-  // extra items (this thread's penalised values, then its singletons) join
-  // the segment of the largest bin at or below their y; a segment records
-  // the range of penalised values it received
-  {
-    const uint32_t n_own = ns > (uint32_t)tid ? (ns - (uint32_t)tid + kSB - 1) / kSB : 0u;
-    const uint32_t first = lo_p >= 0 ? (uint32_t)lo_p : (uint32_t)kHSegBins;
-    const uint32_t last_p = hi_p >= 0 ? (uint32_t)hi_p + 1u : 0u;
-#pragma unroll 1
-    for (uint32_t i = first; i < (uint32_t)kHSegBins + n_own; ++i) {
-      if (i >= last_p && i < (uint32_t)kHSegBins) continue;
-      float y;
-      uint32_t c;
-      uint32_t s = 0xFFFFFFFFu;
-      if (i < (uint32_t)kHSegBins) {
-        c = pcnt_of(sm, seg0 + (int)i);
-        if (!c) continue;
-        y = ypbin(seg0 + (int)i);
-      } else {
-        s = (uint32_t)tid + (i - kHSegBins) * kSB;
-        c = 1u;
-        const float x = sm.sx[s];
-        y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
-      }
-      const int bf = place(y);
-      const int sg = bf < 0 ? 0 : bf / kHSegBins;
-      if (s != 0xFFFFFFFFu) {
-        sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
-      } else {
-        atomicMin(&sm.seg_plo[sg], (uint32_t)(seg0 + (int)i));
-        atomicMax(&sm.seg_phi[sg], (uint32_t)(seg0 + (int)i) + 1u);
-      }
-      atomicAdd(&sm.segw[sg], (unsigned long long)c * detexp_fix(y - m));
-      atomicAdd(&sm.segc[sg], c);
-    }
+  ymax = wave_max_f(ymax);
+  odd = __ballot(odd) != 0ull;
+  __syncthreads();
+  if (lane == 0) {
+    sm.red_m[wid] = ymax;
+    sm.red_u[wid] = odd ? 1u : 0u;
   }
   __syncthreads();
-  W_t += sm.segw[tid];
-  C_t += sm.segc[tid];
+  float m = kNegInf;
+  uint32_t any_odd = 0;
+#pragma unroll
+  for (int w = 0; w < kSW; ++w) {
+    m = fmaxf(m, sm.red_m[w]);
+    any_odd |= sm.red_u[w];
+  }
+  if (any_odd) return false;
+  // Pass B: weights.  Bins sum per segment (row of 16 lanes); penalised
+  // values and singletons join the segment of the largest bin at or below
+  // their y, and a segment records the range of penalised values it got.
+#pragma unroll 1
+  for (int kb = 0; kb < kHBins / kSB; ++kb) {
+    const int bb = kb * kSB + wid * kWave + lane;
+    const uint32_t c = sm.cnt[bb], pc = pcnt_of(sm, bb);
+    if (__ballot((c | pc) != 0u) == 0ull) continue;
+    const unsigned long long w = c ? (unsigned long long)c * detexp_fix(ybin(bb) - m) : 0ull;
+    const unsigned long long rw = row_scan_u64(w);
+    if ((lane & 15) == 15 && rw) atomicAdd(&sm.segw[bb >> 4], rw);
+    if (pc) {
+      const float y = ypbin(bb);
+      const int bf = place(y);
+      const int sg = bf < 0 ? 0 : bf / kHSegBins;
+      atomicMin(&sm.seg_plo[sg], (uint32_t)bb);
+      atomicMax(&sm.seg_phi[sg], (uint32_t)bb + 1u);
+      atomicAdd(&sm.segw[sg], (unsigned long long)pc * detexp_fix(y - m));
+      atomicAdd(&sm.segc[sg], pc);
+    }
+  }
+  for (uint32_t s = tid; s < ns; s += kSB) {
+    const float x = sm.sx[s];
+    const float y = is_pen(sm.sid[s]) ? ypen(x) : x / Tc + 0.0f;
+    const int bf = place(y);
+    sm.sbin[s] = bf < 0 ? (uint16_t)0xFFFFu : (uint16_t)bf;
+    const int sg = bf < 0 ? 0 : bf / kHSegBins;
+    atomicAdd(&sm.segw[sg], detexp_fix(y - m));
+    atomicAdd(&sm.segc[sg], 1u);
+  }
+  __syncthreads();
+  const unsigned long long W_t = sm.segw[tid];
+  const uint32_t C_t = sm.segc[tid];
   // count / weight of all segments above this one (descending order)
   unsigned long long aW, W_all;
   uint32_t aC, n_valid;
@@ -1446,20 +1497,25 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       // the segment's bins, in scalar registers
       float ys[kHSegBins];
       uint32_t cs[kHSegBins];
+      unsigned long long wq[kHSegBins];
       {
         const float yl = lane < kHSegBins ? ybin(b0 + lane) : 0.0f;
         const uint32_t cl = lane < kHSegBins ? sm.cnt[b0 + lane] : 0u;
+        const unsigned long long wl = cl ? detexp_fix(yl - m) : 0ull;
 #pragma unroll
         for (int q = 0; q < kHSegBins; ++q) {
           ys[q] = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(yl), q));
           cs[q] = (uint32_t)__builtin_amdgcn_readlane((int)cl, q);
+          wq[q] = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wl >> 32), q)
+                   << 32) |
+                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wl, q);
         }
       }
       const int plo = (int)sm.seg_plo[t], phi = (int)sm.seg_phi[t];
       bool bad = phi - plo > kHPenSpan;
       // extra items: the penalised values placed here, and the segment's
       // singletons
-      uint32_t k = 0;
+      uint32_t k = 0, k_pen = 0;
       if (!bad) {
         for (int base = plo; base < phi; base += kWave) {
           const int p = base + lane;
@@ -1469,6 +1525,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
           if (ext && pos < (uint32_t)kHXCap) sm.xcode[pos] = (uint32_t)(kHBins + p);
           k += (uint32_t)__builtin_popcountll(mk);
         }
+        k_pen = k;
         for (uint32_t base = 0; base < ns; base += kWave) {
           const uint32_t s = base + (uint32_t)lane;
           bool in = false;
@@ -1485,11 +1542,14 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       }
       wave_lds_sync();
       // extras sorted by rank: key = (ord y, ~tag), tag = id << 12 | slot for
-      // a singleton, 2^30 | p for a penalised value
+      // a singleton, 2^30 | p for a penalised value.  Penalised values come
+      // in rising order, so without singletons reading them backwards sorts
+      // them.
       const bool have = !bad && (uint32_t)lane < k;
+      const bool presorted = k_pen == k;
       unsigned long long key = 0;
       if (have) {
-        const uint32_t code = sm.xcode[lane];
+        const uint32_t code = sm.xcode[presorted ? k - 1u - (uint32_t)lane : (uint32_t)lane];
         float y;
         uint32_t tag;
         if (code >= (uint32_t)kHBins) {
@@ -1504,7 +1564,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         }
         key = ((unsigned long long)ord32(y) << 32) | (unsigned long long)(0xFFFFFFFFu - tag);
       }
-      if (k > 1u && !bad) key = wave_sort_desc_u64(key);
+      if (k > 1u && !bad && !presorted) key = wave_sort_desc_u64(key);
       const uint32_t tag_me = 0xFFFFFFFFu - (uint32_t)key;
       const uint32_t oy_me = (uint32_t)(key >> 32);
       const float y_me = have ? unord32(oy_me) : kNegInf;
@@ -1561,7 +1621,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
             if (lane == 0) {
               const uint32_t pos = nzb + (uint32_t)__builtin_popcountll(above_x);
               const int32_t ax = merged ? sm.aux_q[q] : -1;
-              sm.it_w[pos] = detexp_fix(ys[q] - m);
+              sm.it_w[pos] = wq[q];
               sm.it_c[pos] = cs[q] + (ax >= 0 ? pcnt_of(sm, ax) : 0u);
               sm.it_ref[pos] = b0 + q;
               sm.it_aux[pos] = ax;
@@ -1702,7 +1762,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   }
   if (need1 || need2) {
     const int64_t nv8 = (V + 7) / 8;
-    const int64_t span = (((nv8 + kSB - 1) / kSB) + 7) & ~(int64_t)7;
+    const int64_t span = (nv8 + kSB - 1) / kSB;
     const int64_t t0 = (int64_t)tid * span < nv8 ? (int64_t)tid * span : nv8;
     const int64_t t1 = t0 + span < nv8 ? t0 + span : nv8;
     // members of the two items among the 8 tokens (bit patterns hv) from e0:
@@ -1750,15 +1810,15 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     const int64_t vlast = t1 < nvec ? t1 : nvec;  // full vectors of the range end here
     uint32_t c1 = 0, c2 = 0;
 #pragma unroll 1
-    for (int64_t s = t0; s < vlast; s += 4) {
-      u32x4 buf[4];
+    for (int64_t s = t0; s < vlast; s += 8) {
+      u32x4 buf[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const int64_t vi = s + i < vlast ? s + i : vlast - 1;
         buf[i] = *reinterpret_cast<const u32x4*>(row + vi * 8);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         if (s + i < vlast) {
           uint32_t hv[8];
           words(buf[i], hv);
