@@ -272,6 +272,16 @@ template <int R>
 __device__ __forceinline__ void wave_sort_desc(uint32_t (&v)[R]) {
   const int lane = threadIdx.x & (kWave - 1);
   constexpr int N = kWave * R;
+  auto xch = [](uint32_t x, int j) __attribute__((always_inline)) -> uint32_t {
+    switch (j) {
+      case 1: return lane_xor<1>(x);
+      case 2: return lane_xor<2>(x);
+      case 4: return lane_xor<4>(x);
+      case 8: return lane_xor<8>(x);
+      case 16: return lane_xor<16>(x);
+      default: return lane_xor<32>(x);
+    }
+  };
 #pragma unroll
   for (int k = 2; k <= N; k <<= 1) {
 #pragma unroll
@@ -290,7 +300,7 @@ __device__ __forceinline__ void wave_sort_desc(uint32_t (&v)[R]) {
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const uint32_t w = (uint32_t)__shfl_xor((int)v[r], j, kWave);
+          const uint32_t w = xch(v[r], j);
           const bool desc = ((r * kWave + lane) & k) == 0;
           const bool lower = (lane & j) == 0;
           v[r] = desc == lower ? max(v[r], w) : min(v[r], w);
@@ -945,16 +955,22 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     lse_fold_block_max<false, kFG, E>(st, x, cm);
 #pragma unroll
     for (int k = 0; k < kFG; ++k) {
-      const bool hit = gm[k] >= theta && gm[k] > kNegInf;
+      // this vector's allow bits: bit (o*E) & 31 of the chunk's word o*E >> 5
+      // (o = its offset in the chunk), held by that lane; with a mask the
+      // hit test uses the largest allowed value
+      uint32_t ab = (1u << E) - 1u;
+      float gh = gm[k];
+      if (kMask) {
+        const uint32_t o = (uint32_t)(k * kWave + lane) * E;
+        ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & ((1u << E) - 1u);
+        float xm[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) xm[j] = (ab >> j) & 1u ? x[k][j] : kNegInf;
+        gh = vec_max<E>(xm);
+      }
+      const bool hit = gh >= theta && gh > kNegInf;
       const unsigned long long m = __ballot(hit);
       if (m) {
-        // this vector's allow bits: bit (o*E) & 31 of the chunk's word o*E >> 5
-        // (o = its offset in the chunk), held by that lane
-        uint32_t ab = (1u << E) - 1u;
-        if (kMask) {
-          const uint32_t o = (uint32_t)(k * kWave + lane) * E;
-          ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & ((1u << E) - 1u);
-        }
         if (hit) {
           const uint32_t pos = qn + (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
           sm.u.st.qv[wid][pos] = raw[k];

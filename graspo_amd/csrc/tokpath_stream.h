@@ -34,6 +34,26 @@ __device__ __forceinline__ float max3raw(float a, float b, float c) {
   return d;
 }
 
+// Value of lane (l ^ J) for lane l, without an LDS round trip where the
+// pattern allows: DPP quad permutes for J = 1, 2, row shifts for J = 4, 8,
+// a swizzle for J = 16, and a permute only for J = 32.
+template <int J>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else if constexpr (J == 4 || J == 8) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x100 + J, 0xF, 0xF, false);
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x110 + J, 0xF, 0xF, false);
+    return (threadIdx.x & J) ? dn : up;  // row_shl:J reads lane + J, row_shr:J lane - J
+  } else if constexpr (J == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);  // and 0x1F, xor 0x10
+  } else {
+    return (uint32_t)__shfl_xor((int)v, J, kWave);
+  }
+}
+
 // maximum of one vector's E logits (same NaN rule as max3raw)
 template <int E>
 __device__ __forceinline__ float vec_max(const float (&x)[E]) {
