@@ -13,6 +13,9 @@ Prints ONE JSON line.  ``value`` is sampled rows/s of the sampler kernel;
 come from HIP events recorded around each launch on the stream the kernels
 are launched on (torch's current stream, which the ops use).
 
+``rooflines.logprob_backward`` times the logprob gradient kernel over the
+same [8192, 248320] logits (read once, bf16 gradient written once).
+
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
 [64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
 512 MB buffer written between launches to evict the MALL.
@@ -33,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 REPO = os.path.dirname(os.path.abspath(__file__))
 SAMPLER_KERNEL = "sampler_split_kernel<bf16>"
 LOGPROB_KERNEL = "logprob_entropy_kernel<bf16>"
+BACKWARD_KERNEL = "logprob_backward_kernel<bf16>"
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_large_vocab.md")
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
@@ -237,7 +241,29 @@ def main() -> int:
         "per_config": None,
         "cpu_baseline": None,
     }
-    del lx, lt, batches, wl_b
+    # the gradient of the logprob pass (one read of the logits, one write of
+    # the bf16 gradient), the kernel behind the autograd backward
+    g_lp = torch.randn(N, device=dev)
+    lp_f, _, _ = ops.logprob_entropy(lx, lt)
+    lse = lx.gather(1, lt.long().unsqueeze(1)).squeeze(1).float() - lp_f
+    grad = torch.empty_like(lx)
+    for _ in range(2):
+        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
+    bevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(10)]
+    for e0, e1 in bevs:
+        e0.record()
+        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
+        e1.record()
+    torch.cuda.synchronize()
+    b_ms = sum(a.elapsed_time(b) for a, b in bevs) / len(bevs)
+    b_bytes = 2 * N * V * lx.element_size() + N * (lt.element_size() + 4 + 4)
+    b_gbs = b_bytes / (b_ms * 1e-3) / 1e9
+    line["rooflines"]["logprob_backward"] = {
+        "bound": "hbm", "achieved": round(b_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(b_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(BACKWARD_KERNEL),
+        "kernel": BACKWARD_KERNEL, "algorithmic_bytes": b_bytes, "avg_us": round(b_ms * 1e3, 2)}
+    del lx, lt, batches, wl_b, grad, g_lp, lse, lp_f
     if not args.no_per_config:
         flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
         line["per_config"] = {

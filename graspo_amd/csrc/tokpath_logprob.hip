@@ -115,6 +115,124 @@ __global__ void lse_finalize_kernel(const float* __restrict__ state, int64_t N,
   if (out_H) out_H[n] = ln_s - t / s;
 }
 
+// ---------------------------------------------------------------- backward
+//
+// d logprob / d x_i = [i == target] - p_i with p_i = exp(x_i - lse), so the
+// gradient of a loss with dL/dlogprob = g per row is g * ([i == t] - p_i):
+// one read of the row and one write of the gradient in the logits' dtype.
+// A row with g == 0 (an ignored SFT position) is written as zeros without
+// reading it.
+
+// fp32 -> bf16 bit pattern, round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  const uint32_t u = f2u(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC0u : r;
+}
+
+template <typename T>
+struct GradOut;
+template <>
+struct GradOut<uint16_t> {
+  // 8 gradients -> one 16-byte vector of bf16
+  __device__ static __forceinline__ u32x4 pack(const float (&g)[8]) {
+    u32x4 v;
+    v.x = bf16_rne(g[0]) | (bf16_rne(g[1]) << 16);
+    v.y = bf16_rne(g[2]) | (bf16_rne(g[3]) << 16);
+    v.z = bf16_rne(g[4]) | (bf16_rne(g[5]) << 16);
+    v.w = bf16_rne(g[6]) | (bf16_rne(g[7]) << 16);
+    return v;
+  }
+  __device__ static __forceinline__ void put(uint16_t* p, int64_t i, float g) {
+    p[i] = (uint16_t)bf16_rne(g);
+  }
+};
+template <>
+struct GradOut<_Float16> {
+  __device__ static __forceinline__ u32x4 pack(const float (&g)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const _Float16 lo = (_Float16)g[2 * k], hi = (_Float16)g[2 * k + 1];
+      w[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    u32x4 v;
+    v.x = w[0];
+    v.y = w[1];
+    v.z = w[2];
+    v.w = w[3];
+    return v;
+  }
+  __device__ static __forceinline__ void put(_Float16* p, int64_t i, float g) {
+    p[i] = (_Float16)g;
+  }
+};
+template <>
+struct GradOut<float> {
+  __device__ static __forceinline__ u32x4 pack(const float (&g)[4]) {
+    u32x4 v;
+    v.x = f2u(g[0]);
+    v.y = f2u(g[1]);
+    v.z = f2u(g[2]);
+    v.w = f2u(g[3]);
+    return v;
+  }
+  __device__ static __forceinline__ void put(float* p, int64_t i, float g) { p[i] = g; }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
+    const T* __restrict__ logits, int64_t V, int64_t row_stride, int64_t col_offset,
+    const void* __restrict__ targets, int t64, const float* __restrict__ grad_lp,
+    const float* __restrict__ lse_in, T* __restrict__ grad, int64_t grad_stride) {
+  constexpr int E = Vec<T>::kE;
+  const int64_t n = blockIdx.x;
+  const T* row = logits + n * row_stride;
+  T* grow = grad + n * grad_stride;
+  const float g = grad_lp[n];
+  const int64_t tgt = load_target(targets, t64, n) - col_offset;  // outside [0, V): no one-hot term
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) | reinterpret_cast<uintptr_t>(grow)) & 15u) == 0;
+  const int64_t nvec = vec_ok ? V / E : 0;
+  u32x4* gv = reinterpret_cast<u32x4*>(grow);
+  if (g == 0.0f) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int64_t vi = threadIdx.x; vi < nvec; vi += kLpBlock) __builtin_nontemporal_store(z, gv + vi);
+    for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) GradOut<T>::put(grow, i, 0.0f);
+    return;
+  }
+  // p_i = 2^(x_i log2 e - lse log2 e); the one-hot term is added where i == t
+  const float lse = lse_in[n];
+  const float c = lse * kLog2e;
+  const float ng = -g;
+  stream_vectors<T, kLpBlock, kLpVecs, true>(
+      row, 0, nvec, [&](float(&x)[kLpVecs][E], int64_t vbase, bool last) {
+#pragma unroll
+        for (int k = 0; k < kLpVecs; ++k) {
+          const int64_t vi = vbase + (int64_t)k * kLpBlock;
+          if (last && vi >= nvec) continue;
+          float gr[E];
+#pragma unroll
+          for (int j = 0; j < E; ++j)
+            gr[j] = ng * __builtin_amdgcn_exp2f(__builtin_fmaf(x[k][j], kLog2e, -c));
+          const int64_t d = tgt - vi * E;
+          if (d >= 0 && d < E) {
+            // g (1 - p_t) as -g expm1(x_t - lse): no cancellation when p_t ~ 1
+#pragma unroll
+            for (int j = 0; j < E; ++j)
+              if (j == (int)d) gr[j] = -g * expm1f(x[k][j] - lse);
+          }
+          __builtin_nontemporal_store(GradOut<T>::pack(gr), gv + vi);
+        }
+      });
+  for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) {
+    const float xi = Elem<T>::get(row, i);
+    const float gi = i == tgt ? -g * expm1f(xi - lse)
+                              : ng * __builtin_amdgcn_exp2f(__builtin_fmaf(xi, kLog2e, -c));
+    GradOut<T>::put(grow, i, gi);
+  }
+}
+
 }  // namespace gtp
 
 using namespace gtp;
@@ -194,3 +312,40 @@ extern "C" int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_l
 }
 
 extern "C" const char* gtp_version(void) { return "graspo_tokpath 0.2 gfx950"; }
+
+extern "C" int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N, int64_t V,
+                                         int64_t row_stride, int64_t col_offset,
+                                         const void* targets, int targets_int64,
+                                         const float* grad_logprob, const float* lse, void* grad,
+                                         int64_t grad_stride, void* stream) {
+  if (N < 0 || V <= 0 || row_stride < V || grad_stride < V ||
+      (N > 0 && (!logits || !targets || !grad_logprob || !lse || !grad)))
+    return GTP_ERR_INVALID_ARGUMENT;
+  if (N > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
+  if (N == 0) return GTP_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)N), block(kLpBlock);
+  switch (dtype) {
+    case GTP_DTYPE_BF16:
+      hipLaunchKernelGGL(logprob_backward_kernel<uint16_t>, grid, block, 0, s,
+                         reinterpret_cast<const uint16_t*>(logits), V, row_stride, col_offset,
+                         targets, targets_int64, grad_logprob, lse,
+                         reinterpret_cast<uint16_t*>(grad), grad_stride);
+      break;
+    case GTP_DTYPE_F16:
+      hipLaunchKernelGGL(logprob_backward_kernel<_Float16>, grid, block, 0, s,
+                         reinterpret_cast<const _Float16*>(logits), V, row_stride, col_offset,
+                         targets, targets_int64, grad_logprob, lse,
+                         reinterpret_cast<_Float16*>(grad), grad_stride);
+      break;
+    case GTP_DTYPE_F32:
+      hipLaunchKernelGGL(logprob_backward_kernel<float>, grid, block, 0, s,
+                         reinterpret_cast<const float*>(logits), V, row_stride, col_offset,
+                         targets, targets_int64, grad_logprob, lse,
+                         reinterpret_cast<float*>(grad), grad_stride);
+      break;
+    default:
+      return GTP_ERR_INVALID_ARGUMENT;
+  }
+  return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+}

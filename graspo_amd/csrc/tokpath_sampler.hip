@@ -1003,104 +1003,6 @@ __device__ __forceinline__ uint32_t nth_bit(uint32_t m, uint32_t n) {
   return (uint32_t)__builtin_ctz(m);
 }
 
-// Orders one wave's LDS writes before its later LDS reads from other lanes.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Lane l receives lane l - s of its row of 16 (row_shr), lane 15 of the
-// previous row (row_bcast:15, rows 1 and 3) or lane 31 (row_bcast:31, rows
-// 2 and 3); lanes without a source read 0.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint32_t dpp_take(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xF, false);
-}
-// Inclusive scans over the 64 lanes of a wave (DPP, no LDS round trip).
-__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
-  x += dpp_take<0x111, 0xF>(x);
-  x += dpp_take<0x112, 0xF>(x);
-  x += dpp_take<0x114, 0xF>(x);
-  x += dpp_take<0x118, 0xF>(x);
-  x += dpp_take<0x142, 0xA>(x);
-  x += dpp_take<0x143, 0xC>(x);
-  return x;
-}
-__device__ __forceinline__ unsigned long long wave_scan_u64(unsigned long long x) {
-#define GTP_SCAN64_STEP(ctrl, rm)                                                    \
-  {                                                                                  \
-    const uint32_t lo = dpp_take<ctrl, rm>((uint32_t)x);                             \
-    const uint32_t hi = dpp_take<ctrl, rm>((uint32_t)(x >> 32));                     \
-    x += ((unsigned long long)hi << 32) | lo;                                        \
-  }
-  GTP_SCAN64_STEP(0x111, 0xF)
-  GTP_SCAN64_STEP(0x112, 0xF)
-  GTP_SCAN64_STEP(0x114, 0xF)
-  GTP_SCAN64_STEP(0x118, 0xF)
-  GTP_SCAN64_STEP(0x142, 0xA)
-  GTP_SCAN64_STEP(0x143, 0xC)
-#undef GTP_SCAN64_STEP
-  return x;
-}
-__device__ __forceinline__ uint32_t lane63_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
-}
-__device__ __forceinline__ unsigned long long lane63_u64(unsigned long long v) {
-  return ((unsigned long long)lane63_u32((uint32_t)(v >> 32)) << 32) | lane63_u32((uint32_t)v);
-}
-// Sums within each row of 16 lanes (inclusive; lane 15 of a row holds the
-// row's total).
-__device__ __forceinline__ uint32_t row_scan_u32(uint32_t x) {
-  x += dpp_take<0x111, 0xF>(x);
-  x += dpp_take<0x112, 0xF>(x);
-  x += dpp_take<0x114, 0xF>(x);
-  x += dpp_take<0x118, 0xF>(x);
-  return x;
-}
-__device__ __forceinline__ unsigned long long row_scan_u64(unsigned long long x) {
-#define GTP_ROW64_STEP(ctrl)                                                         \
-  {                                                                                  \
-    const uint32_t lo = dpp_take<ctrl, 0xF>((uint32_t)x);                            \
-    const uint32_t hi = dpp_take<ctrl, 0xF>((uint32_t)(x >> 32));                    \
-    x += ((unsigned long long)hi << 32) | lo;                                        \
-  }
-  GTP_ROW64_STEP(0x111)
-  GTP_ROW64_STEP(0x112)
-  GTP_ROW64_STEP(0x114)
-  GTP_ROW64_STEP(0x118)
-#undef GTP_ROW64_STEP
-  return x;
-}
-// Wave maximum of a float (every lane gets it); NaN inputs are ignored.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dpp_take_max(float v) {
-  return u2f((uint32_t)__builtin_amdgcn_update_dpp((int)0xFF800000u, (int)f2u(v), kCtrl, kRowMask,
-                                                   0xF, false));
-}
-__device__ __forceinline__ float wave_max_f(float x) {
-  x = fmaxf(x, dpp_take_max<0x111, 0xF>(x));
-  x = fmaxf(x, dpp_take_max<0x112, 0xF>(x));
-  x = fmaxf(x, dpp_take_max<0x114, 0xF>(x));
-  x = fmaxf(x, dpp_take_max<0x118, 0xF>(x));
-  x = fmaxf(x, dpp_take_max<0x142, 0xA>(x));
-  x = fmaxf(x, dpp_take_max<0x143, 0xC>(x));
-  return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(x), kWave - 1));
-}
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dpp_take_f(float v) {
-  return u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), kCtrl, kRowMask, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum_f(float x) {
-  x += dpp_take_f<0x111, 0xF>(x);
-  x += dpp_take_f<0x112, 0xF>(x);
-  x += dpp_take_f<0x114, 0xF>(x);
-  x += dpp_take_f<0x118, 0xF>(x);
-  x += dpp_take_f<0x142, 0xA>(x);
-  x += dpp_take_f<0x143, 0xC>(x);
-  return u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(x), kWave - 1));
-}
-
 // wave sort of 64-bit keys, descending (one per lane)
 __device__ __forceinline__ unsigned long long wave_sort_desc_u64(unsigned long long v) {
   const int lane = threadIdx.x & (kWave - 1);

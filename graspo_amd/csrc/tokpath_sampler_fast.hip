@@ -1035,11 +1035,8 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       }
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    nval += (uint32_t)__shfl_xor((int)nval, o, kWave);
-    mx16 = max(mx16, (uint32_t)__shfl_xor((int)mx16, o, kWave));
-  }
+  nval = lane63_u32(wave_scan_u32(nval));
+  mx16 = (uint32_t)wave_max_f((float)mx16);  // 16-bit keys are exact in fp32
   if (lane == 0) {
     sm.redu[tid / kWave] = nval;
     if (mx16) atomicMax(&sm.kmax16, mx16);

@@ -1,6 +1,6 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
-// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, lse_partial,
+// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, lse_partial,
 // lse_finalize}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
@@ -216,6 +216,43 @@ std::tuple<at::Tensor, at::Tensor> lse_finalize(const at::Tensor& state, int64_t
   return {lp, H};
 }
 
+at::Tensor logprob_backward(const at::Tensor& logits, const at::Tensor& targets,
+                            const at::Tensor& grad_logprob, const at::Tensor& lse,
+                            int64_t col_offset, const c10::optional<at::Tensor>& out,
+                            int64_t stream) {
+  check_rows(logits, "logits");
+  const int64_t N = logits.size(0), V = logits.size(1);
+  TORCH_CHECK(V > 0, "graspo_tokpath.logprob_backward: empty vocabulary");
+  int t64 = 0;
+  const void* tp = targets_ptr(logits, targets, N, &t64);
+  for (const at::Tensor* t : {&grad_logprob, &lse}) {
+    check_same_device(logits, *t, "grad_logprob / lse");
+    TORCH_CHECK(t->scalar_type() == at::kFloat && t->dim() == 1 && t->size(0) == N &&
+                    t->is_contiguous(),
+                "graspo_tokpath.logprob_backward: grad_logprob and lse must be float32 [N] "
+                "contiguous");
+  }
+  at::Tensor grad;
+  if (out.has_value()) {
+    grad = *out;
+    check_same_device(logits, grad, "out");
+    TORCH_CHECK(grad.scalar_type() == logits.scalar_type() && grad.dim() == 2 &&
+                    grad.size(0) == N && grad.size(1) == V && (V == 1 || grad.stride(1) == 1) &&
+                    grad.stride(0) >= V,
+                "graspo_tokpath.logprob_backward: out must be [N, V] of the logits' dtype "
+                "with unit column stride");
+  } else {
+    grad = at::empty({N, V}, logits.options());
+  }
+  const int64_t gstride = N > 1 ? grad.stride(0) : V;
+  const int rc = gtp_logprob_backward_rows(
+      logits.data_ptr(), dtype_code(logits), N, V, row_stride_of(logits), col_offset, tp, t64,
+      grad_logprob.data_ptr<float>(), lse.data_ptr<float>(), grad.data_ptr(), gstride,
+      reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_logprob_backward_rows");
+  return grad;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(graspo_tokpath, m) {
@@ -231,4 +268,8 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "bool accumulate, int stream) -> ()",
       &lse_partial);
   m.def("lse_finalize(Tensor state, int stream) -> (Tensor, Tensor)", &lse_finalize);
+  m.def(
+      "logprob_backward(Tensor logits, Tensor targets, Tensor grad_logprob, Tensor lse, "
+      "int col_offset, Tensor(a!)? out, int stream) -> Tensor",
+      &logprob_backward);
 }

@@ -45,15 +45,14 @@ class _SequenceLogProbs(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         logits, output_ids, lp = ctx.saved_tensors
-        # d logprob_t / d x = onehot(t) - softmax(x); softmax from the saved
-        # lse = x_t - logprob_t
-        x = logits.float()
-        xt = x.gather(-1, output_ids.unsqueeze(-1))
-        lse = xt - lp.unsqueeze(-1)
-        g = grad_out.unsqueeze(-1).float()
-        grad = -g * torch.exp(x - lse)
-        grad.scatter_add_(-1, output_ids.unsqueeze(-1), g)
-        return grad.to(logits.dtype), None
+        # d logprob_t / d x = onehot(t) - softmax(x), with softmax from the
+        # saved lse = x_t - logprob_t: one read of the logits, one write
+        V = logits.shape[-1]
+        rows = logits.reshape(-1, V)
+        t = output_ids.reshape(-1).to(torch.int64)
+        lse = rows.gather(1, t.unsqueeze(1)).squeeze(1).float() - lp.reshape(-1)
+        grad = ops.logprob_backward(rows, t, grad_out.reshape(-1), lse)
+        return grad.view(logits.shape), None
 
 
 def sequence_log_probs_from_logits(logits: torch.Tensor, output_ids: torch.Tensor) -> torch.Tensor:

@@ -17,6 +17,7 @@ from __future__ import annotations
 import importlib
 
 from . import graspo_loss as _loss
+from . import sft_loss as _sft
 from . import tensor_utils as _tu
 
 _TU = "graspo.backends.graspoflow.tensor_utils"
@@ -34,6 +35,9 @@ TARGETS: dict[str, tuple[str, ...]] = {
     "graspo.backends.graspoflow.models.qwen35_36.training": _LOGPROB_NAMES,
     "graspo.backends.graspoflow.transformer_adapter": _LOGPROB_NAMES,
     "graspo.core.graspo_loss": ("sequence_log_probs_from_logits",),
+    # imported inside transformer_adapter.compute_loss (transformer_adapter.py:467),
+    # so the module attribute is what that call resolves
+    "graspo.core.sft_loss": ("sft_cross_entropy_loss",),
 }
 
 REPLACEMENTS = {
@@ -42,6 +46,7 @@ REPLACEMENTS = {
     "_broadcast_and_pad_finished": _tu._broadcast_and_pad_finished,
     "_selected_token_log_probs_from_hidden": _tu._selected_token_log_probs_from_hidden,
     "sequence_log_probs_from_logits": _loss.sequence_log_probs_from_logits,
+    "sft_cross_entropy_loss": _sft.sft_cross_entropy_loss,
 }
 
 _saved: dict[tuple[str, str], object] = {}

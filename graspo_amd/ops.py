@@ -102,6 +102,24 @@ def logprob_entropy(logits: torch.Tensor, targets: torch.Tensor):
     return ops.logprob_entropy(logits, targets.contiguous(), _stream(logits))
 
 
+def logprob_backward(logits: torch.Tensor, targets: torch.Tensor, grad_logprob: torch.Tensor,
+                     lse: torch.Tensor, col_offset: int = 0,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """d/dlogits of sum_n grad_logprob[n] * log_softmax(logits[n])[targets[n]]:
+    g * (onehot - softmax) in the logits' dtype, [N, V] (written into ``out``
+    when given: [N, V], unit column stride).  ``lse`` is each row's
+    log-sum-exp over the whole vocabulary; for a vocabulary chunk pass its
+    first column as ``col_offset``.  Rows with g == 0 are zeros (not read)."""
+    ops = load()
+    logits = _as_rows(logits)
+    targets = targets.reshape(-1)
+    if targets.dtype not in (torch.int32, torch.int64):
+        targets = targets.to(torch.int64)
+    return ops.logprob_backward(
+        logits, targets.contiguous(), grad_logprob.reshape(-1).to(torch.float32).contiguous(),
+        lse.reshape(-1).to(torch.float32).contiguous(), int(col_offset), out, _stream(logits))
+
+
 def lse_partial(logits_chunk: torch.Tensor, targets: torch.Tensor | None, col_offset: int,
                 state: torch.Tensor, accumulate: bool) -> None:
     """Fold a vocabulary chunk into the running (m, s, t, x_target) row state."""

@@ -114,20 +114,16 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         h2, weight, t, lse = ctx.saved_tensors
         g = grad_out.reshape(-1).to(torch.float32)
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        grad_h = grad_w = None
-        if need_h:
-            grad_h = (g.unsqueeze(1) * weight.index_select(0, t).float()).to(h2.dtype)
-        if need_w:
-            grad_w = torch.zeros_like(weight)
-            grad_w.index_add_(0, t, (g.unsqueeze(1) * h2.float()).to(weight.dtype))
+        grad_h = torch.zeros_like(h2) if need_h else None
+        grad_w = torch.empty_like(weight) if need_w else None
         for start in range(0, weight.shape[0], ctx.chunk):
             w_c = weight[start : start + ctx.chunk]
-            p = torch.exp(F.linear(h2, w_c).float() - lse.unsqueeze(1))
-            gp = (g.unsqueeze(1) * p).to(h2.dtype)
+            # g * (onehot - softmax) of this chunk's logits, one kernel pass
+            gc = ops.logprob_backward(F.linear(h2, w_c), t, g, lse, col_offset=start)
             if need_h:
-                grad_h -= gp @ w_c
+                grad_h += gc.to(h2.dtype) @ w_c.to(h2.dtype)
             if need_w:
-                grad_w[start : start + ctx.chunk] -= gp.t() @ h2
+                grad_w[start : start + ctx.chunk] = (gc.t() @ h2.to(gc.dtype)).to(weight.dtype)
         if grad_h is not None:
             grad_h = grad_h.view(*ctx.out_shape, h2.shape[-1])
         return grad_h, grad_w, None, None

@@ -181,6 +181,35 @@ int gtp_lse_partial_rows(const void* logits, int dtype, int64_t N, int64_t Vc,
 int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_logprob,
                           float* out_entropy, void* stream);
 
+/*
+ * gtp_logprob_backward_rows -- gradient of log_softmax(x)[target] with respect
+ * to the logits, scaled by the incoming gradient of each row:
+ *   grad[i] = g * ([i == target - col_offset] - exp(x_i - lse))
+ * written in the logits' dtype (bf16 rounded to nearest even), one read of
+ * the logits and one write of the gradient.
+ *
+ * Replaces the autograd backward of sequence_log_probs_from_logits
+ * src/graspo/core/graspo_loss.py:19-21 and of F.cross_entropy in
+ * sft_cross_entropy_loss src/graspo/core/sft_loss.py:12-34 (both materialise
+ * the [N, V] softmax in fp32), and the per-chunk softmax of the backward of
+ * _selected_token_log_probs_from_hidden tensor_utils.py:167-186 (logits of one
+ * vocabulary chunk, col_offset = its first column).
+ *
+ *   targets       [N] int32 (targets_int64 == 0) or int64; a target outside
+ *                 [col_offset, col_offset + V) adds no one-hot term
+ *   grad_logprob  [N] fp32, g per row; a row with g == 0 is written as zeros
+ *                 without reading its logits (ignored positions)
+ *   lse           [N] fp32, the row's log-sum-exp over the whole vocabulary
+ *   grad          [N, grad_stride] of dtype, 16-byte aligned rows take the
+ *                 vector path
+ */
+int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N,
+                              int64_t V, int64_t row_stride,
+                              int64_t col_offset, const void* targets,
+                              int targets_int64, const float* grad_logprob,
+                              const float* lse, void* grad,
+                              int64_t grad_stride, void* stream);
+
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
 
