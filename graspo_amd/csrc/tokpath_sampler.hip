@@ -962,7 +962,7 @@ struct alignas(16) HistSmem {
   uint32_t pick_c;
   unsigned long long pick_w;
   int32_t res_ref, res_aux, res_j;
-  uint32_t res_c;
+  uint32_t res_c, res_cb;
   unsigned long long res_wb, res_w;
   int32_t id_out[2];
 };
@@ -1388,9 +1388,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   };
   // Resolve segment t (wave 0): its items in rank order.  mode 0: the item
   // holding in-segment rank v; mode 1: the item holding in-segment weight
-  // offset v; mode 2: the number of in-segment ranks whose preceding weight
-  // is <= v (in res_j).  Returns false (block-uniform) when the segment is
-  // outside the bounds of this path.
+  // offset v (the rank inside it is an integer quotient).  Returns false
+  // (block-uniform) when the segment is outside the bounds of this path.
   auto resolve = [&](int t, int mode, unsigned long long v)
                      __attribute__((always_inline)) -> bool {
     __syncthreads();
@@ -1548,7 +1547,6 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         const unsigned long long lw = wt2[0] + wt2[1];
         uint32_t cb = wave_scan_u32(lc) - lc;
         unsigned long long wb = wave_scan_u64(lw) - lw;
-        uint32_t count = 0;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const uint32_t i = 2u * (uint32_t)lane + (uint32_t)q;
@@ -1558,29 +1556,22 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
             if (mode == 0) {
               hit = v >= cb && v < (unsigned long long)cb + c2[q];
               jj = (uint32_t)(v - cb);
-            } else if (mode == 1) {
+            } else {
               hit = v >= wb && v < wb + wt2[q];
-              jj = w2[q] ? (uint32_t)((v - wb) / w2[q]) : 0u;
-            } else if (v >= wb) {
-              const unsigned long long f =
-                  w2[q] ? (v - wb) / w2[q] + 1ull : (unsigned long long)c2[q];
-              count += f < c2[q] ? (uint32_t)f : c2[q];
+              if (hit) jj = (uint32_t)((v - wb) / w2[q]);  // w2 > 0 on a hit
             }
             if (hit) {
               sm.res_ref = sm.it_ref[i];
               sm.res_aux = sm.it_aux[i];
               sm.res_j = (int32_t)jj;
               sm.res_c = c2[q];
+              sm.res_cb = cb;
               sm.res_wb = wb;
               sm.res_w = w2[q];
             }
             cb += c2[q];
             wb += wt2[q];
           }
-        }
-        if (mode == 2) {
-          count = lane63_u32(wave_scan_u32(count));
-          if (lane == 0) sm.res_j = (int32_t)count;
         }
       }
       if (lane < kHSegBins) sm.aux_q[lane] = -1;
@@ -1592,22 +1583,27 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   const bool p_active = a.P > 0.0f && a.P < 1.0f;
   const bool k_active = a.K >= 1 && (uint32_t)a.K < n_valid;
   const uint32_t nk = k_active ? (uint32_t)a.K : n_valid;
-  // Four searches over the rank order, one resolved segment each:
-  // (0) top-k: W_K = S_nk, the weight of the nk best ranks (S_r: the weight
-  //     of the ranks before r);
-  // (1) top-p: R = min(nk, #{r : S_r <= floor(P W_K)});
-  // (2) the last kept rank R - 1, and W' = S_R;
-  // (3) the draw: the rank whose weight interval holds U = floor(u W').
+  // Three searches over the rank order, one resolved segment each
+  // (S_r: the weight of the ranks before r):
+  // (0) top-k: the rank nk - 1, W_K = S_nk;
+  // (1) top-p: the rank r* whose weight interval holds F = floor(P W_K).
+  //     #{r : S_r <= F} = r* + 1, so R = min(nk, r* + 1), and when r* + 1
+  //     <= nk, r* is the last kept rank with W' = S_{r*+1}; otherwise the
+  //     last kept rank is (0)'s with W' = W_K.  Without top-p, R = nk and
+  //     the last kept rank is (0)'s or, without top-k, the last valid rank.
+  // (2) the draw: the rank whose weight interval holds U = floor(u W').
   unsigned long long W_K = W_all, Wp = 0, w_draw = 0;
   uint32_t R = nk;
   int32_t thr_ref = 0, thr_aux = -1, thr_j = 0, drw_ref = 0, drw_aux = -1, drw_j = 0;
   uint32_t thr_c = 0, drw_c = 0;
+  bool have_thr = false;
   for (int step = 0; step < 4; ++step) {
-    if ((step == 0 && !k_active) || (step == 1 && !p_active)) continue;
-    const int mode = step == 1 ? 2 : step == 3 ? 1 : 0;
+    if ((step == 0 && !k_active) || (step == 1 && !p_active) || (step == 2 && have_thr)) continue;
+    // step 2: the last valid rank (neither top-k nor top-p active)
+    const int mode = step == 0 || step == 2 ? 0 : 1;
     const unsigned long long target = step == 0   ? (unsigned long long)(nk - 1u)
                                       : step == 1 ? floor_mul(a.P, W_K)
-                                      : step == 2 ? (unsigned long long)(R - 1u)
+                                      : step == 2 ? (unsigned long long)(nk - 1u)
                                                   : floor_mul(u, Wp);
     pick(mode == 0 ? (C_t && aC <= target && target < (unsigned long long)aC + C_t)
                    : (W_t && aW <= target && target < aW + W_t));
@@ -1615,17 +1611,18 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     if (!resolve(sm.seg_pick, mode, target - (mode == 0 ? sm.pick_c : sm.pick_w))) return false;
     const unsigned long long S_after =
         sm.pick_w + sm.res_wb + (unsigned long long)(sm.res_j + 1) * sm.res_w;
-    if (step == 0) {
-      W_K = S_after;
-    } else if (step == 1) {
-      const uint32_t le = sm.pick_c + (uint32_t)sm.res_j;
-      R = le < nk ? le : nk;
-    } else if (step == 2) {
+    if (step == 0 || step == 2 ||
+        (step == 1 && sm.pick_c + sm.res_cb + (uint32_t)sm.res_j + 1u <= nk)) {
+      if (step == 0) W_K = S_after;
+      if (step == 1) R = sm.pick_c + sm.res_cb + (uint32_t)sm.res_j + 1u;
       thr_ref = sm.res_ref;
       thr_aux = sm.res_aux;
       thr_j = sm.res_j;
       thr_c = sm.res_c;
       Wp = S_after;
+      have_thr = step != 0 || !p_active;
+    } else if (step == 1) {
+      have_thr = true;  // the top-k cut binds: (0)'s rank and W' = W_K stay
     } else {
       drw_ref = sm.res_ref;
       drw_aux = sm.res_aux;
