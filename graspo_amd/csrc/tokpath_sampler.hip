@@ -1395,23 +1395,6 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     __syncthreads();
     if (wid == 0) {
       const int b0 = t * kHSegBins;
-      // the segment's bins, in scalar registers
-      float ys[kHSegBins];
-      uint32_t cs[kHSegBins];
-      unsigned long long wq[kHSegBins];
-      {
-        const float yl = lane < kHSegBins ? ybin(b0 + lane) : 0.0f;
-        const uint32_t cl = lane < kHSegBins ? sm.cnt[b0 + lane] : 0u;
-        const unsigned long long wl = cl ? detexp_fix(yl - m) : 0ull;
-#pragma unroll
-        for (int q = 0; q < kHSegBins; ++q) {
-          ys[q] = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(yl), q));
-          cs[q] = (uint32_t)__builtin_amdgcn_readlane((int)cl, q);
-          wq[q] = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wl >> 32), q)
-                   << 32) |
-                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wl, q);
-        }
-      }
       const int plo = (int)sm.seg_plo[t], phi = (int)sm.seg_phi[t];
       bool bad = phi - plo > kHPenSpan;
       // extra items: the penalised values placed here, and the segment's
@@ -1442,6 +1425,45 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
         bad = k > (uint32_t)kHXCap;
       }
       wave_lds_sync();
+      if (!bad && k == 0) {
+        // no extra items: the segment's bins in descending order (lane l
+        // holds bin 15 - l), counted and weighed by scans in registers
+        const int q = kHSegBins - 1 - lane;
+        const uint32_t c = lane < kHSegBins ? sm.cnt[b0 + q] : 0u;
+        const unsigned long long w = c ? detexp_fix(ybin(b0 + q) - m) : 0ull;
+        const unsigned long long wt = (unsigned long long)c * w;
+        const uint32_t cb = wave_scan_u32(c) - c;
+        const unsigned long long wb = wave_scan_u64(wt) - wt;
+        const bool hit = mode == 0 ? (v >= cb && v < (unsigned long long)cb + c)
+                                   : (v >= wb && v < wb + wt);
+        if (hit) {
+          sm.res_ref = b0 + q;
+          sm.res_aux = -1;
+          sm.res_j = (int32_t)(mode == 0 ? v - cb : (v - wb) / w);  // w > 0 on a weight hit
+          sm.res_c = c;
+          sm.res_cb = cb;
+          sm.res_wb = wb;
+          sm.res_w = w;
+        }
+        if (lane == 0) sm.fallback = 0;
+      } else {
+      // the segment's bins, in scalar registers
+      float ys[kHSegBins];
+      uint32_t cs[kHSegBins];
+      unsigned long long wq[kHSegBins];
+      {
+        const float yl = lane < kHSegBins ? ybin(b0 + lane) : 0.0f;
+        const uint32_t cl = lane < kHSegBins ? sm.cnt[b0 + lane] : 0u;
+        const unsigned long long wl = cl ? detexp_fix(yl - m) : 0ull;
+#pragma unroll
+        for (int q = 0; q < kHSegBins; ++q) {
+          ys[q] = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(yl), q));
+          cs[q] = (uint32_t)__builtin_amdgcn_readlane((int)cl, q);
+          wq[q] = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wl >> 32), q)
+                   << 32) |
+                  (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wl, q);
+        }
+      }
       // extras sorted by rank: key = (ord y, ~tag), tag = id << 12 | slot for
       // a singleton, 2^30 | p for a penalised value.  Penalised values come
       // in rising order, so without singletons reading them backwards sorts
@@ -1576,6 +1598,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       }
       if (lane < kHSegBins) sm.aux_q[lane] = -1;
       if (lane == 0) sm.fallback = bad ? 1 : 0;
+      }
     }
     __syncthreads();
     return sm.fallback == 0;
