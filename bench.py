@@ -16,6 +16,9 @@ are launched on (torch's current stream, which the ops use).
 ``rooflines.logprob_backward`` times the logprob gradient kernel over the
 same [8192, 248320] logits (read once, bf16 gradient written once).
 
+``graspo_loss`` times forward + backward of the fused GRASPO loss against
+the reference's torch expression over [16, 2048] token logprobs.
+
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
 [64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
 512 MB buffer written between launches to evict the MALL.
@@ -145,6 +148,45 @@ def time_sampler_config(cfg: int, dev, iters: int, flush):
     }
 
 
+def time_graspo_loss(dev, B: int = 16, T: int = 2048, iters: int = 50):
+    """Forward + backward of the GRASPO PPO-clip loss over [B, T] token
+    logprobs: the fused kernels against the reference's torch expression
+    (graspo_loss.py:10-16, 45-63) on the same device."""
+    import torch
+
+    from graspo_amd.graspo_loss import GRASPOLoss
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    lp = -torch.rand(B, T, device=dev, generator=g) * 3
+    old = lp + 0.3 * torch.randn(B, T, device=dev, generator=g)
+    adv = torch.randn(B, 1, device=dev, generator=g).expand(B, T).contiguous()
+    mask = torch.rand(B, T, device=dev, generator=g) < 0.7
+
+    def ref(x):
+        ratio = (x - old).exp()
+        loss = -torch.min(ratio * adv, ratio.clamp(0.8, 1.2) * adv)
+        return ((loss * mask).sum(dim=-1) / mask.sum(dim=-1).clamp_min(1)).mean()
+
+    fused = GRASPOLoss(0.2)
+    out = {}
+    for name, fn in (("fused_us", lambda x: fused(x, old, adv, mask)), ("torch_us", ref)):
+        for _ in range(3):
+            x = lp.clone().requires_grad_(True)
+            fn(x).backward()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        xs = [lp.clone().requires_grad_(True) for _ in range(iters)]
+        torch.cuda.synchronize()
+        e0.record()
+        for x in xs:
+            fn(x).backward()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / iters * 1e3, 2)
+    out["shape"] = [B, T]
+    out["what"] = "forward + backward per call, HIP events around 50 back-to-back calls"
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -264,6 +306,7 @@ def main() -> int:
         "frac": round(b_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(BACKWARD_KERNEL),
         "kernel": BACKWARD_KERNEL, "algorithmic_bytes": b_bytes, "avg_us": round(b_ms * 1e3, 2)}
     del lx, lt, batches, wl_b, grad, g_lp, lse, lp_f
+    line["graspo_loss"] = time_graspo_loss(dev)
     if not args.no_per_config:
         flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
         line["per_config"] = {

@@ -1,6 +1,6 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
-// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, lse_partial,
+// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
 // lse_finalize}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
@@ -253,6 +253,71 @@ at::Tensor logprob_backward(const at::Tensor& logits, const at::Tensor& targets,
   return grad;
 }
 
+void check_loss_input(const at::Tensor& t, const at::Tensor& ref, const char* name) {
+  check_same_device(ref, t, name);
+  TORCH_CHECK(t.scalar_type() == at::kFloat && t.is_contiguous() && t.sizes() == ref.sizes(),
+              "graspo_tokpath.graspo_loss: ", name, " must be float32, contiguous, of the shape "
+              "of log_probs");
+}
+
+// fp32 weights or bool / uint8 0-1 bytes, of the shape of log_probs
+const void* loss_mask(const c10::optional<at::Tensor>& mask, const at::Tensor& logp, int* u8) {
+  *u8 = 0;
+  if (!mask.has_value()) return nullptr;
+  const at::Tensor& m = *mask;
+  check_same_device(logp, m, "action_mask");
+  TORCH_CHECK((m.scalar_type() == at::kFloat || m.scalar_type() == at::kBool ||
+               m.scalar_type() == at::kByte) &&
+                  m.is_contiguous() && m.sizes() == logp.sizes(),
+              "graspo_tokpath.graspo_loss: action_mask must be float32, bool or uint8, "
+              "contiguous, of the shape of log_probs");
+  *u8 = m.scalar_type() != at::kFloat;
+  return m.data_ptr();
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> graspo_loss_forward(
+    const at::Tensor& logp, const at::Tensor& old_logp, const at::Tensor& adv,
+    const c10::optional<at::Tensor>& mask, double clip_lo, double clip_hi, int64_t stream) {
+  TORCH_CHECK(logp.is_cuda() && logp.dim() == 2 && logp.size(0) > 0 && logp.size(1) > 0,
+              "graspo_tokpath.graspo_loss: log_probs must be a non-empty [B, T] GPU tensor");
+  check_loss_input(logp, logp, "log_probs");
+  check_loss_input(old_logp, logp, "old_log_probs");
+  check_loss_input(adv, logp, "advantages");
+  int mu8 = 0;
+  const void* mp = loss_mask(mask, logp, &mu8);
+  const int64_t B = logp.size(0), T = logp.size(1);
+  at::Tensor loss = at::empty({}, logp.options());
+  at::Tensor per_seq = at::empty({B}, logp.options());
+  at::Tensor inv_den = at::empty({B}, logp.options());
+  const int rc = gtp_graspo_loss_forward(
+      logp.data_ptr<float>(), old_logp.data_ptr<float>(), adv.data_ptr<float>(), mp, mu8, B, T,
+      (float)clip_lo, (float)clip_hi, loss.data_ptr<float>(), per_seq.data_ptr<float>(),
+      inv_den.data_ptr<float>(), reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_graspo_loss_forward");
+  return {loss, per_seq, inv_den};
+}
+
+at::Tensor graspo_loss_backward(const at::Tensor& logp, const at::Tensor& old_logp,
+                                const at::Tensor& adv, const c10::optional<at::Tensor>& mask,
+                                const at::Tensor& inv_denom, const at::Tensor& grad_loss,
+                                double clip_lo, double clip_hi, int64_t stream) {
+  check_loss_input(old_logp, logp, "old_log_probs");
+  check_loss_input(adv, logp, "advantages");
+  int mu8 = 0;
+  const void* mp = loss_mask(mask, logp, &mu8);
+  const int64_t B = logp.size(0), T = logp.size(1);
+  TORCH_CHECK(inv_denom.scalar_type() == at::kFloat && inv_denom.numel() == B &&
+                  grad_loss.scalar_type() == at::kFloat && grad_loss.numel() == 1,
+              "graspo_tokpath.graspo_loss_backward: bad inv_denom / grad_loss");
+  at::Tensor grad = at::empty_like(logp);
+  const int rc = gtp_graspo_loss_backward(
+      logp.data_ptr<float>(), old_logp.data_ptr<float>(), adv.data_ptr<float>(), mp, mu8,
+      inv_denom.data_ptr<float>(), grad_loss.data_ptr<float>(), B, T, (float)clip_lo,
+      (float)clip_hi, grad.data_ptr<float>(), reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_graspo_loss_backward");
+  return grad;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(graspo_tokpath, m) {
@@ -272,4 +337,13 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "logprob_backward(Tensor logits, Tensor targets, Tensor grad_logprob, Tensor lse, "
       "int col_offset, Tensor(a!)? out, int stream) -> Tensor",
       &logprob_backward);
+  m.def(
+      "graspo_loss_forward(Tensor log_probs, Tensor old_log_probs, Tensor advantages, "
+      "Tensor? action_mask, float clip_lo, float clip_hi, int stream) -> (Tensor, Tensor, Tensor)",
+      &graspo_loss_forward);
+  m.def(
+      "graspo_loss_backward(Tensor log_probs, Tensor old_log_probs, Tensor advantages, "
+      "Tensor? action_mask, Tensor inv_denom, Tensor grad_loss, float clip_lo, float clip_hi, "
+      "int stream) -> Tensor",
+      &graspo_loss_backward);
 }

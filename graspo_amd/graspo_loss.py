@@ -7,6 +7,7 @@ are the consumers of its output, kept as small torch expressions.
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 from torch import nn
 
@@ -82,10 +83,33 @@ def masked_mean(
     return (tensor * weights).sum(dim=dim) / mask.sum(dim=dim).clamp_min(1)
 
 
+class _GRASPOLossFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, log_probs, old_log_probs, advantages, action_mask, clip_lo, clip_hi):
+        loss, _, inv_denom = ops.graspo_loss_forward(
+            log_probs, old_log_probs, advantages, action_mask, clip_lo, clip_hi)
+        ctx.save_for_backward(log_probs, old_log_probs, advantages, action_mask, inv_denom)
+        ctx.clip = (clip_lo, clip_hi)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        log_probs, old_log_probs, advantages, action_mask, inv_denom = ctx.saved_tensors
+        grad = None
+        if ctx.needs_input_grad[0]:
+            grad = ops.graspo_loss_backward(
+                log_probs, old_log_probs, advantages, action_mask, inv_denom,
+                grad_loss.reshape(1).float().contiguous(), *ctx.clip)
+        return grad, None, None, None, None, None
+
+
 class GRASPOLoss(nn.Module):
     """PPO-clip surrogate over token logprobs (reference: graspo_loss.py:45-63):
     -min(r A, clip(r, 1-eps, 1+eps) A) with r = exp(logp - logp_old), averaged
-    per sequence over the action mask, then over sequences."""
+    per sequence over the action mask (masked_mean, graspo_loss.py:10-16),
+    then over sequences.  Two fused kernels forward, one backward (d/dlogp
+    only: the old logprobs, advantages and mask are data, as in every
+    reference call site)."""
 
     def __init__(self, policy_ratio_clip_eps: float = 0.2) -> None:
         super().__init__()
@@ -96,11 +120,23 @@ class GRASPOLoss(nn.Module):
         log_probs: torch.Tensor,
         old_log_probs: torch.Tensor,
         advantages: torch.Tensor,
-        action_mask: torch.Tensor,
+        action_mask: torch.Tensor | None,
     ) -> torch.Tensor:
         eps = self.policy_ratio_clip_eps
-        ratio = torch.exp(log_probs - old_log_probs)
-        unclipped = ratio * advantages
-        clipped = torch.clamp(ratio, 1.0 - eps, 1.0 + eps) * advantages
-        per_token = -torch.minimum(unclipped, clipped)
-        return masked_mean(per_token, action_mask, dim=-1).mean()
+        # torch rounds the Python bounds 1 -/+ eps to fp32 the same way
+        lo, hi = float(np.float32(1.0 - eps)), float(np.float32(1.0 + eps))
+        T = log_probs.shape[-1]
+        shape = log_probs.shape
+        lp = log_probs.reshape(-1, T)
+        dt = lp.dtype
+
+        def rows(t, keep_dtype=False):
+            t = torch.broadcast_to(t, shape).reshape(-1, T)
+            return (t if keep_dtype else t.float()).contiguous()
+
+        mask = None
+        if action_mask is not None:
+            mask = rows(action_mask, keep_dtype=action_mask.dtype in (torch.bool, torch.uint8))
+        loss = _GRASPOLossFn.apply(lp.float().contiguous(), rows(old_log_probs.detach()),
+                                   rows(advantages.detach()), mask, lo, hi)
+        return loss.to(dt)

@@ -34,7 +34,9 @@ TARGETS: dict[str, tuple[str, ...]] = {
     "graspo.backends.graspoflow.models.qwen35_36.logprobs": _LOGPROB_NAMES,
     "graspo.backends.graspoflow.models.qwen35_36.training": _LOGPROB_NAMES,
     "graspo.backends.graspoflow.transformer_adapter": _LOGPROB_NAMES,
-    "graspo.core.graspo_loss": ("sequence_log_probs_from_logits",),
+    # GRASPOLoss is imported inside the adapters' __init__ (transformer_adapter.py:118),
+    # so install() must run before the adapter is built
+    "graspo.core.graspo_loss": ("sequence_log_probs_from_logits", "GRASPOLoss"),
     # imported inside transformer_adapter.compute_loss (transformer_adapter.py:467),
     # so the module attribute is what that call resolves
     "graspo.core.sft_loss": ("sft_cross_entropy_loss",),
@@ -47,6 +49,7 @@ REPLACEMENTS = {
     "_selected_token_log_probs_from_hidden": _tu._selected_token_log_probs_from_hidden,
     "sequence_log_probs_from_logits": _loss.sequence_log_probs_from_logits,
     "sft_cross_entropy_loss": _sft.sft_cross_entropy_loss,
+    "GRASPOLoss": _loss.GRASPOLoss,
 }
 
 _saved: dict[tuple[str, str], object] = {}

@@ -120,6 +120,25 @@ def logprob_backward(logits: torch.Tensor, targets: torch.Tensor, grad_logprob: 
         lse.reshape(-1).to(torch.float32).contiguous(), int(col_offset), out, _stream(logits))
 
 
+def graspo_loss_forward(log_probs: torch.Tensor, old_log_probs: torch.Tensor,
+                        advantages: torch.Tensor, action_mask: torch.Tensor | None,
+                        clip_lo: float, clip_hi: float):
+    """(loss, per-sequence masked means, 1 / max(1, mask sums)) of the
+    GRASPO PPO-clip surrogate over fp32 [B, T] inputs."""
+    ops = load()
+    return ops.graspo_loss_forward(log_probs, old_log_probs, advantages, action_mask,
+                                   float(clip_lo), float(clip_hi), _stream(log_probs))
+
+
+def graspo_loss_backward(log_probs, old_log_probs, advantages, action_mask, inv_denom,
+                         grad_loss, clip_lo: float, clip_hi: float) -> torch.Tensor:
+    """d(loss)/d(log_probs) scaled by ``grad_loss`` (a 1-element fp32 tensor)."""
+    ops = load()
+    return ops.graspo_loss_backward(log_probs, old_log_probs, advantages, action_mask, inv_denom,
+                                    grad_loss, float(clip_lo), float(clip_hi),
+                                    _stream(log_probs))
+
+
 def lse_partial(logits_chunk: torch.Tensor, targets: torch.Tensor | None, col_offset: int,
                 state: torch.Tensor, accumulate: bool) -> None:
     """Fold a vocabulary chunk into the running (m, s, t, x_target) row state."""

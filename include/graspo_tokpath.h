@@ -210,6 +210,37 @@ int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N,
                               const float* lse, void* grad,
                               int64_t grad_stride, void* stream);
 
+/*
+ * gtp_graspo_loss_forward / gtp_graspo_loss_backward -- the GRASPO PPO-clip
+ * surrogate over token logprobs, fused:
+ *   loss = mean_b( sum_t m l / max(1, sum_t m) ),
+ *   l = -min(r A, clamp(r, clip_lo, clip_hi) A),  r = exp(logp - old_logp)
+ * Replaces GRASPOLoss.forward src/graspo/core/graspo_loss.py:45-63 with
+ * masked_mean :10-16 (about ten elementwise and reduction launches) by two
+ * kernels forward and one backward.
+ *
+ *   logp, old_logp, adv  [B, T] fp32 contiguous
+ *   mask                 [B, T] fp32 weights (mask_u8 == 0), bytes of 0/1
+ *                        (mask_u8 != 0, e.g. a bool tensor), or NULL (all ones)
+ *   clip_lo, clip_hi     1 - eps and 1 + eps as fp32
+ *   out_loss             [1] fp32; per_seq [B] fp32 (each sequence's masked
+ *                        mean); inv_denom [B] fp32 (1 / max(1, sum_t m)),
+ *                        which the backward reads
+ *   grad_loss            [1] fp32, d(out)/d(loss) from the caller
+ *   grad_logp            [B, T] fp32: d(out)/d(logp); old_logp, adv and the
+ *                        mask get no gradient (as in the reference's use)
+ */
+int gtp_graspo_loss_forward(const float* logp, const float* old_logp,
+                            const float* adv, const void* mask, int mask_u8, int64_t B,
+                            int64_t T, float clip_lo, float clip_hi,
+                            float* out_loss, float* per_seq, float* inv_denom,
+                            void* stream);
+int gtp_graspo_loss_backward(const float* logp, const float* old_logp,
+                             const float* adv, const void* mask, int mask_u8,
+                             const float* inv_denom, const float* grad_loss,
+                             int64_t B, int64_t T, float clip_lo,
+                             float clip_hi, float* grad_logp, void* stream);
+
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
 

@@ -97,10 +97,21 @@ def test_integration_rebinds_and_restores(monkeypatch):
         assert getattr(sys.modules[mod_name], a) is f
 
 
+def test_graspo_loss_has_no_cpu_path():
+    """The fused loss runs on the GPU only; CPU tensors are rejected."""
+    from graspo_amd.graspo_loss import GRASPOLoss
+
+    x = torch.zeros(2, 3)
+    with pytest.raises(RuntimeError):
+        GRASPOLoss(policy_ratio_clip_eps=0.2)(x, x, x, torch.ones(2, 3, dtype=torch.bool))
+
+
+@pytest.mark.gpu
 def test_graspo_loss_known_answer():
     """The reference's own known-answer case (tests/core/test_graspo_loss.py:8-24)."""
     from graspo_amd.graspo_loss import GRASPOLoss
 
+    dev = torch.device("cuda:0")
     log_probs = torch.tensor([[0.0, 0.2, -0.1], [0.1, -0.3, 0.4]])
     old = torch.tensor([[-0.1, 0.1, -0.1], [0.0, -0.1, 0.2]])
     adv = torch.tensor([[1.0, 1.0, 1.0], [-0.5, -0.5, -0.5]])
@@ -108,7 +119,8 @@ def test_graspo_loss_known_answer():
     r = torch.exp(log_probs - old)
     per = -torch.min(r * adv, r.clamp(0.8, 1.2) * adv)
     want = ((per * mask).sum(-1) / mask.sum(-1)).mean()
-    got = GRASPOLoss(policy_ratio_clip_eps=0.2)(log_probs, old, adv, mask)
+    got = GRASPOLoss(policy_ratio_clip_eps=0.2)(log_probs.to(dev), old.to(dev), adv.to(dev),
+                                                mask.to(dev)).cpu()
     assert torch.allclose(got, want)
     # the same case worked by hand: row 0 keeps ratios e^0.1 (inside the clip)
     # on two tokens; row 1 (advantage -0.5) keeps the unclipped e^0.2 term
