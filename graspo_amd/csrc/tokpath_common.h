@@ -108,6 +108,13 @@ __device__ __forceinline__ uint64_t detexp_fix(float d) {
   return q;
 }
 
+// log_softmax(x)_i = x_i - m - ln s evaluated in fp64 and rounded once:
+// |x - m| can be far above 2^24 (huge logits), where two fp32 roundings
+// would differ from the correctly rounded value by an ulp.
+__device__ __forceinline__ float raw_logprob(float x, float m, float ln_s) {
+  return (float)(((double)x - (double)m) - (double)ln_s);
+}
+
 // floor(f * W) for fp32 f in [0, 1), exact (f = M * 2^-sh with M < 2^24).
 __device__ __forceinline__ uint64_t floor_mul(float f, uint64_t W) {
   if (!(f > 0.0f)) return 0ull;

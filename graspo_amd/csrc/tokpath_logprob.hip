@@ -31,8 +31,7 @@ __device__ __forceinline__ void lse_fold_one(Lse3& st, float x) {
     st.m = x;
   }
   if (x != x) st.s = __builtin_nanf("");
-  const float mL = st.m == kNegInf ? 0.0f : st.m * kLog2e;
-  const float d = __builtin_fmaf(x, kLog2e, -mL);
+  const float d = (x - (st.m == kNegInf ? 0.0f : st.m)) * kLog2e;
   const float e = __builtin_amdgcn_exp2f(d);
   st.s += e;
   st.t = __builtin_fmaf(e, fmaxf(d, -256.0f), st.t);
@@ -73,7 +72,7 @@ __global__ __launch_bounds__(kLpBlock) void logprob_entropy_kernel(
   const Lse3 st = block_lse3<kLpBlock>(lp_thread_state<T>(row, V), red);
   if (threadIdx.x == 0) {
     const float ln_s = __builtin_amdgcn_logf(st.s) * kLn2;
-    out_lp[n] = tgt_ok ? xt - st.m - ln_s : __builtin_nanf("");
+    out_lp[n] = tgt_ok ? raw_logprob(xt, st.m, ln_s) : __builtin_nanf("");
     if (out_H) out_H[n] = ln_s - kLn2 * st.t / st.s;
     if (out_status) out_status[n] = tgt_ok ? GTP_ROW_OK : GTP_ROW_BAD_TARGET;
   }
@@ -111,7 +110,7 @@ __global__ void lse_finalize_kernel(const float* __restrict__ state, int64_t N,
   if (n >= N) return;
   const float m = state[n * 4 + 0], s = state[n * 4 + 1], t = state[n * 4 + 2], xt = state[n * 4 + 3];
   const float ln_s = __builtin_amdgcn_logf(s) * kLn2;
-  if (out_lp) out_lp[n] = xt - m - ln_s;
+  if (out_lp) out_lp[n] = raw_logprob(xt, m, ln_s);
   if (out_H) out_H[n] = ln_s - t / s;
 }
 
@@ -201,9 +200,8 @@ __global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
     for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) GradOut<T>::put(grow, i, 0.0f);
     return;
   }
-  // p_i = 2^(x_i log2 e - lse log2 e); the one-hot term is added where i == t
+  // p_i = 2^((x_i - lse) log2 e); the one-hot term is added where i == t
   const float lse = lse_in[n];
-  const float c = lse * kLog2e;
   const float ng = -g;
   stream_vectors<T, kLpBlock, kLpVecs, true>(
       row, 0, nvec, [&](float(&x)[kLpVecs][E], int64_t vbase, bool last) {
@@ -214,7 +212,7 @@ __global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
           float gr[E];
 #pragma unroll
           for (int j = 0; j < E; ++j)
-            gr[j] = ng * __builtin_amdgcn_exp2f(__builtin_fmaf(x[k][j], kLog2e, -c));
+            gr[j] = ng * __builtin_amdgcn_exp2f((x[k][j] - lse) * kLog2e);
           const int64_t d = tgt - vi * E;
           if (d >= 0 && d < E) {
             // g (1 - p_t) as -g expm1(x_t - lse): no cancellation when p_t ~ 1
@@ -228,7 +226,7 @@ __global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
   for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) {
     const float xi = Elem<T>::get(row, i);
     const float gi = i == tgt ? -g * expm1f(xi - lse)
-                              : ng * __builtin_amdgcn_exp2f(__builtin_fmaf(xi, kLog2e, -c));
+                              : ng * __builtin_amdgcn_exp2f((xi - lse) * kLog2e);
     GradOut<T>::put(grow, i, gi);
   }
 }

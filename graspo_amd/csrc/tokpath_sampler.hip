@@ -145,12 +145,12 @@ __device__ __forceinline__ void lse_fold(LseState& st, const float (&x)[NG][8], 
   if (mn == kNegInf) return;
   if (mn != st.m && st.s > 0.0f) st.s *= __builtin_amdgcn_exp2f((st.m - mn) * kLog2e);
   st.m = mn;
-  const float mL = mn * kLog2e;
+  const float mb = mn;
   float s = 0.0f;
 #pragma unroll
   for (int k = 0; k < NG; ++k)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[k][j], kLog2e, -mL));
+    for (int j = 0; j < 8; ++j) s += __builtin_amdgcn_exp2f((x[k][j] - mb) * kLog2e);
   st.s += s;
 }
 
@@ -464,7 +464,8 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     lse_fold<kSG>(ls, x, cm);
   }
   const LseState row_lse = block_lse(sm, ls);
-  const float lse_raw = row_lse.m + __builtin_amdgcn_logf(row_lse.s) * kLn2;
+  // logprob = x - m - ln s, rounded once (raw_logprob)
+  const float lse_m = row_lse.m, lse_ln = __builtin_amdgcn_logf(row_lse.s) * kLn2;
   const bool nonfinite = (row_lse.s != row_lse.s) || row_lse.m == kPosInf;
 
   int32_t status = GTP_ROW_OK;
@@ -573,7 +574,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
       if (r.greedy) {
         if (tid == 0) {
           const int32_t id = rank_key_id(k0);
-          write_row(a, b, GTP_ROW_OK, id, sm.cand_x[sm.order[0]] - lse_raw, 0.0f, 1, m, id);
+          write_row(a, b, GTP_ROW_OK, id, raw_logprob(sm.cand_x[sm.order[0]], lse_m, lse_ln), 0.0f, 1, m, id);
         }
         return;
       }
@@ -625,7 +626,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
         const int32_t id = rank_key_id(sm.cand_key[ci]);
         const unsigned long long kt = sm.cand_key[sm.order[R - 1]];
         const float slp = (float)::log((double)ws / (double)Wp);
-        write_row(a, b, GTP_ROW_OK, id, sm.cand_x[ci] - lse_raw, slp, R, rank_key_y(kt),
+        write_row(a, b, GTP_ROW_OK, id, raw_logprob(sm.cand_x[ci], lse_m, lse_ln), slp, R, rank_key_y(kt),
                   rank_key_id(kt));
       }
       return;
@@ -875,7 +876,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   if (tid == 0) {
     const bool in_row = id_draw >= 0 && id_draw < r.V;
     const float xd = in_row ? Elem<T>::get(r.x, id_draw) : __builtin_nanf("");
-    write_row(a, b, GTP_ROW_OK, id_draw, xd - lse_raw, (float)slp, kept, y_thr, (int32_t)id_thr);
+    write_row(a, b, GTP_ROW_OK, id_draw, raw_logprob(xd, lse_m, lse_ln), (float)slp, kept, y_thr, (int32_t)id_thr);
   }
 }
 
@@ -1261,7 +1262,8 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     lm = mb;
     ls = sb;
   }
-  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+  // logprob = x - m - ln s, rounded once (raw_logprob)
+  const float lse_m = lm, lse_ln = __builtin_amdgcn_logf(ls) * kLn2;
   int32_t status = GTP_ROW_OK;
   if (ls != ls || lm == kPosInf)
     status = GTP_ROW_NONFINITE;
@@ -1821,7 +1823,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     }
     const float x_draw = u2f((uint32_t)row[id_draw] << 16);
     const float slp = (float)::log((double)w_draw / (double)Wp);
-    write_row(a, b, GTP_ROW_OK, id_draw, x_draw - lse_raw, slp, (int32_t)R, y_thr, id_thr);
+    write_row(a, b, GTP_ROW_OK, id_draw, raw_logprob(x_draw, lse_m, lse_ln), slp, (int32_t)R, y_thr, id_thr);
   }
   return true;
 }

@@ -578,7 +578,8 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   const int lane = threadIdx.x;
   if (lane >= kWave) return;
   const float u = fa.greedy ? 0.0f : a.uniforms[b];
-  const float lse_raw = lm + __builtin_amdgcn_logf(ls) * kLn2;
+  // logprob = x - m - ln s, rounded once (raw_logprob)
+  const float lse_m = lm, lse_ln = __builtin_amdgcn_logf(ls) * kLn2;
   int32_t status = GTP_ROW_OK;
   if (ls != ls || lm == kPosInf)
     status = GTP_ROW_NONFINITE;
@@ -599,7 +600,7 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   if (fa.greedy) {
     if (lane == 0) {
       const int32_t id = rank_key_id(k0);
-      write_out(a, b, GTP_ROW_OK, id, sm.fx[0] - lse_raw, 0.0f, 1, m, id);
+      write_out(a, b, GTP_ROW_OK, id, raw_logprob(sm.fx[0], lse_m, lse_ln), 0.0f, 1, m, id);
     }
     return;
   }
@@ -628,7 +629,7 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   if (lane == 0) {
     const unsigned long long kt = sm.fkey[R - 1u];
     const float slp = __builtin_amdgcn_logf((float)((double)(hi - lo) / (double)Wp)) * kLn2;
-    write_out(a, b, GTP_ROW_OK, rank_key_id(sm.fkey[rs]), sm.fx[rs] - lse_raw, slp, (int32_t)R,
+    write_out(a, b, GTP_ROW_OK, rank_key_id(sm.fkey[rs]), raw_logprob(sm.fx[rs], lse_m, lse_ln), slp, (int32_t)R,
               rank_key_y(kt), rank_key_id(kt));
   }
 }

@@ -238,23 +238,33 @@ __device__ __forceinline__ void lse_fold_block_max(Lse3& st, const float (&x)[NG
     }
     st.m = cm;
   }
-  // all -inf so far: any finite base keeps d = -inf (weight 0) and NaN = NaN
-  const float mL = st.m == kNegInf ? 0.0f : st.m * kLog2e;
+  // all -inf so far: any finite base keeps d = -inf (weight 0) and NaN = NaN.
+  // Below |m| = 1024 the base-2 exponent is one fma, x log2e - m log2e (the
+  // rounding of m log2e costs at most 2^-14 of a term, 3e-5 relative); above
+  // it x - m is taken first, exact for x near m at any magnitude.
+  const float mb = st.m == kNegInf ? 0.0f : st.m;
   float s0 = 0.0f, s1 = 0.0f, t0 = 0.0f, t1 = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NG; ++k) {
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const float d = __builtin_fmaf(x[k][j], kLog2e, -mL);
-      const float e = __builtin_amdgcn_exp2f(d);
-      if ((k * E + j) & 1) {
-        s1 += e;
-        if (kEntropy) t1 = __builtin_fmaf(e, fmaxf(d, -256.0f), t1);
-      } else {
-        s0 += e;
-        if (kEntropy) t0 = __builtin_fmaf(e, fmaxf(d, -256.0f), t0);
-      }
+  auto term = [&](float d, int i) __attribute__((always_inline)) {
+    const float e = __builtin_amdgcn_exp2f(d);
+    if (i & 1) {
+      s1 += e;
+      if (kEntropy) t1 = __builtin_fmaf(e, fmaxf(d, -256.0f), t1);
+    } else {
+      s0 += e;
+      if (kEntropy) t0 = __builtin_fmaf(e, fmaxf(d, -256.0f), t0);
     }
+  };
+  if (__builtin_fabsf(mb) < 1024.0f) {
+    const float mL = mb * kLog2e;
+#pragma unroll
+    for (int k = 0; k < NG; ++k)
+#pragma unroll
+      for (int j = 0; j < E; ++j) term(__builtin_fmaf(x[k][j], kLog2e, -mL), k * E + j);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NG; ++k)
+#pragma unroll
+      for (int j = 0; j < E; ++j) term((x[k][j] - mb) * kLog2e, k * E + j);
   }
   st.s += s0 + s1;
   if (kEntropy) st.t += t0 + t1;
