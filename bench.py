@@ -19,6 +19,10 @@ same [8192, 248320] logits (read once, bf16 gradient written once).
 ``graspo_loss`` times forward + backward of the fused GRASPO loss against
 the reference's torch expression over [16, 2048] token logprobs.
 
+``decode_loop`` times the generation loop's own per-token work at the
+[256, 248320] bf16 shape: the decode-loop drop-in against the reference's
+loop body, both on this library's sampler, with a stand-in model.
+
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
 [64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
 512 MB buffer written between launches to evict the MALL.
@@ -187,6 +191,71 @@ def time_graspo_loss(dev, B: int = 16, T: int = 2048, iters: int = 50):
     return out
 
 
+def time_decode_loop(dev, B: int = 256, V: int = 248320, steps: int = 24):
+    """Per-token cost of the generation loop's own work at [B, V] bf16 logits:
+    the decode-loop drop-in (graspo_amd.decode_loop) against the reference's
+    loop body (models/qwen3/adapter.py:283-311: logits.float(), sampler,
+    pad, cat, EOS update, bool(finished.all())) on the same sampler.  The
+    model is a stand-in that returns resident logits, so only the loop is
+    timed; no row reaches EOS, so both loops run every step."""
+    import torch
+
+    from graspo_amd import decode_loop as dl
+    from graspo_amd import tensor_utils as tu
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    logits = (torch.randn(B, 1, V, device=dev, generator=g) * 3.0).to(torch.bfloat16)
+    seq0 = torch.randint(0, V, (B, 64), device=dev, generator=g)
+    eos, pad = V + 7, 0  # never sampled
+
+    class _Model:
+        def __call__(self, ids, attention_mask=None, past_key_values=None, use_cache=False):
+            return (logits, 0) if use_cache else logits
+
+    class _Adapter:
+        model = _Model()
+
+        def _sync_timing(self):
+            pass
+
+    def reference_loop(n):
+        sequences = seq0.clone()
+        finished = torch.zeros(B, dtype=torch.bool, device=dev)
+        out, pkv = _Adapter.model(sequences, attention_mask=sequences.ne(pad), use_cache=True)
+        for _ in range(n):
+            nt = tu._next_token_from_logits(out.float()[:, -1, :], temperature=0.7, top_p=0.9)
+            nt = tu._broadcast_and_pad_finished(nt, finished, pad)
+            sequences = torch.cat([sequences, nt.unsqueeze(1)], dim=1)
+            finished |= nt.eq(eos)
+            if bool(finished.all()):
+                break
+            out, pkv = _Adapter.model(nt.unsqueeze(1), attention_mask=sequences.ne(pad),
+                                      past_key_values=pkv, use_cache=True)
+        return sequences
+
+    def fused_loop(n):
+        finished = torch.zeros(B, dtype=torch.bool, device=dev)
+        return dl.generate_group_with_kv_cache(
+            _Adapter(), sequences=seq0, finished=finished, eos_token_id=eos, pad_token_id=pad,
+            max_new_tokens=n, temperature=0.7, top_p=0.9)[0]
+
+    res = {}
+    for name, fn in (("fused_us_per_step", fused_loop), ("reference_loop_us_per_step",
+                                                         reference_loop)):
+        fn(3)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s = fn(steps)
+        torch.cuda.synchronize()
+        res[name] = round((time.perf_counter() - t0) / steps * 1e6, 1)
+        assert s.shape == (B, 64 + steps)
+    res["shape"] = [B, V]
+    res["what"] = (f"wall time per token over a {steps}-token loop, KV-cache form, T 0.7, "
+                   "top-p 0.9, bf16 logits resident (the reference body samples their fp32 "
+                   "copy)")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +376,7 @@ def main() -> int:
         "kernel": BACKWARD_KERNEL, "algorithmic_bytes": b_bytes, "avg_us": round(b_ms * 1e3, 2)}
     del lx, lt, batches, wl_b, grad, g_lp, lse, lp_f
     line["graspo_loss"] = time_graspo_loss(dev)
+    line["decode_loop"] = time_decode_loop(dev)
     if not args.no_per_config:
         flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
         line["per_config"] = {

@@ -182,12 +182,12 @@ struct LseState {
 };
 __device__ __forceinline__ LseState lse_merge(LseState a, LseState b) {
   float m = fmaxf(a.m, b.m);
+  // NaN sums must survive the merge (they flag non-finite rows), also when
+  // no finite value has been seen (a row of NaN and -inf only)
+  if (a.s != a.s || b.s != b.s) return {m, __builtin_nanf("")};
   if (m == kNegInf) return {kNegInf, 0.0f};
   float sa = a.s == 0.0f ? 0.0f : a.s * __builtin_amdgcn_exp2f((a.m - m) * kLog2e);
   float sb = b.s == 0.0f ? 0.0f : b.s * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
-  // NaN sums must survive the merge (they flag non-finite rows)
-  if (a.s != a.s) sa = a.s;
-  if (b.s != b.s) sb = b.s;
   return {m, sa + sb};
 }
 __device__ __forceinline__ LseState wave_lse(LseState v) {

@@ -1,7 +1,7 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
-// lse_finalize}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lse_finalize, decode_update}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -318,6 +318,63 @@ at::Tensor graspo_loss_backward(const at::Tensor& logp, const at::Tensor& old_lo
   return grad;
 }
 
+// one [B] byte flag tensor (bool or uint8) or a [B, >col] column target
+uint8_t* byte_arg(const at::Tensor& t, const at::Tensor& ids, const char* name) {
+  check_same_device(ids, t, name);
+  TORCH_CHECK(t.scalar_type() == at::kBool || t.scalar_type() == at::kByte,
+              "graspo_tokpath.decode_update: ", name, " must be bool or uint8");
+  return static_cast<uint8_t*>(t.data_ptr());
+}
+
+void decode_update(const at::Tensor& ids, const c10::optional<at::Tensor>& status,
+                   const at::Tensor& finished, int64_t eos_token_id, int64_t pad_token_id,
+                   const c10::optional<at::Tensor>& seq, const c10::optional<at::Tensor>& attn,
+                   int64_t col, const at::Tensor& flags, int64_t stream) {
+  TORCH_CHECK(ids.is_cuda(), "graspo_tokpath.decode_update: ids must be a GPU tensor");
+  TORCH_CHECK(ids.scalar_type() == at::kLong && ids.dim() == 1 && ids.is_contiguous(),
+              "graspo_tokpath.decode_update: ids must be int64 [B]");
+  const int64_t B = ids.size(0);
+  TORCH_CHECK(finished.dim() == 1 && finished.size(0) == B && finished.is_contiguous(),
+              "graspo_tokpath.decode_update: finished must be [B], contiguous");
+  uint8_t* fin = byte_arg(finished, ids, "finished");
+  const int32_t* st = nullptr;
+  if (status.has_value()) {
+    check_same_device(ids, *status, "status");
+    TORCH_CHECK(status->scalar_type() == at::kInt && status->numel() == B && status->is_contiguous(),
+                "graspo_tokpath.decode_update: status must be int32 [B]");
+    st = status->data_ptr<int32_t>();
+  }
+  int64_t* sp = nullptr;
+  int64_t s_stride = 0;
+  if (seq.has_value()) {
+    const auto& s = *seq;
+    check_same_device(ids, s, "sequences");
+    TORCH_CHECK(s.scalar_type() == at::kLong && s.dim() == 2 && s.size(0) == B &&
+                    s.size(1) > col && (B <= 1 || s.stride(1) == 1),
+                "graspo_tokpath.decode_update: sequences must be int64 [B, > col] with "
+                "contiguous rows");
+    sp = s.data_ptr<int64_t>();
+    s_stride = B > 1 ? s.stride(0) : s.size(1);
+  }
+  uint8_t* ap = nullptr;
+  int64_t a_stride = 0;
+  if (attn.has_value()) {
+    const auto& a = *attn;
+    ap = byte_arg(a, ids, "attention_mask");
+    TORCH_CHECK(a.dim() == 2 && a.size(0) == B && a.size(1) > col && (B <= 1 || a.stride(1) == 1),
+                "graspo_tokpath.decode_update: attention_mask must be [B, > col] with contiguous "
+                "rows");
+    a_stride = B > 1 ? a.stride(0) : a.size(1);
+  }
+  check_same_device(ids, flags, "flags");
+  TORCH_CHECK(flags.scalar_type() == at::kInt && flags.numel() >= 2 && flags.is_contiguous(),
+              "graspo_tokpath.decode_update: flags must be int32 [2]");
+  const int rc = gtp_decode_update_rows(ids.data_ptr<int64_t>(), st, B, eos_token_id,
+                                        pad_token_id, fin, sp, s_stride, ap, a_stride, col,
+                                        flags.data_ptr<int32_t>(), reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_decode_update_rows");
+}
+
 }  // namespace
 
 TORCH_LIBRARY(graspo_tokpath, m) {
@@ -346,4 +403,9 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "Tensor? action_mask, Tensor inv_denom, Tensor grad_loss, float clip_lo, float clip_hi, "
       "int stream) -> Tensor",
       &graspo_loss_backward);
+  m.def(
+      "decode_update(Tensor ids, Tensor? status, Tensor(a!) finished, int eos_token_id, "
+      "int pad_token_id, Tensor(b!)? sequences, Tensor(c!)? attention_mask, int col, "
+      "Tensor(d!) flags, int stream) -> ()",
+      &decode_update);
 }

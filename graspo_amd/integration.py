@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import importlib
 
+from . import decode_loop as _dl
 from . import graspo_loss as _loss
 from . import sft_loss as _sft
 from . import tensor_utils as _tu
@@ -52,16 +53,57 @@ REPLACEMENTS = {
     "GRASPOLoss": _loss.GRASPOLoss,
 }
 
+# module -> class -> decode-loop methods replaced on that class (the loops
+# call the sampler, pad, track EOS and test all-finished each token)
+_TEXT_LOOPS = ("_generate_group_with_kv_cache", "_generate_group_full_forward")
+METHOD_TARGETS: dict[str, dict[str, tuple[str, ...]]] = {
+    "graspo.backends.graspoflow.models.qwen3.adapter": {"Qwen3Adapter": _TEXT_LOOPS},
+    "graspo.backends.graspoflow.models.qwen35_36.generation": {
+        "_Qwen35GenerationMethods": _TEXT_LOOPS
+        + ("_generate_multimodal_with_kv_cache", "_generate_multimodal_full_forward"),
+    },
+}
+
+METHOD_REPLACEMENTS = {
+    "_generate_group_with_kv_cache": _dl.generate_group_with_kv_cache,
+    "_generate_group_full_forward": _dl.generate_group_full_forward,
+    "_generate_multimodal_with_kv_cache": _dl.generate_multimodal_with_kv_cache,
+    "_generate_multimodal_full_forward": _dl.generate_multimodal_full_forward,
+}
+
 _saved: dict[tuple[str, str], object] = {}
+_saved_methods: dict[tuple[str, str, str], object] = {}
 
 
-def install(targets: dict[str, tuple[str, ...]] | None = None, *, strict: bool = False):
-    """Rebind the hot-path names in every importable target module.
+def install(targets: dict[str, tuple[str, ...]] | None = None, *, strict: bool = False,
+            methods: dict[str, dict[str, tuple[str, ...]]] | None = None):
+    """Rebind the hot-path names in every importable target module, and the
+    decode-loop methods on the adapter classes.
 
-    Returns the list of ``(module, name)`` pairs that were replaced.  With
-    ``strict`` a module that cannot be imported raises; otherwise it is
-    skipped (a model family that is not installed)."""
+    Returns the list of ``(module, name)`` pairs (``(module, class.method)``
+    for methods) that were replaced.  With ``strict`` a module that cannot be
+    imported raises; otherwise it is skipped (a model family that is not
+    installed)."""
     done = []
+    for mod_name, classes in (METHOD_TARGETS if methods is None else methods).items():
+        try:
+            mod = importlib.import_module(mod_name)
+        except ImportError:
+            if strict:
+                raise
+            continue
+        for cls_name, names in classes.items():
+            cls = getattr(mod, cls_name, None)
+            if cls is None:
+                continue
+            for name in names:
+                if name not in cls.__dict__:
+                    continue
+                key = (mod_name, cls_name, name)
+                if key not in _saved_methods:
+                    _saved_methods[key] = cls.__dict__[name]
+                setattr(cls, name, METHOD_REPLACEMENTS[name])
+                done.append((mod_name, f"{cls_name}.{name}"))
     for mod_name, names in (targets or TARGETS).items():
         try:
             mod = importlib.import_module(mod_name)
@@ -82,6 +124,10 @@ def install(targets: dict[str, tuple[str, ...]] | None = None, *, strict: bool =
 
 def uninstall() -> None:
     """Restore every name :func:`install` replaced."""
+    for (mod_name, cls_name, name), orig in list(_saved_methods.items()):
+        cls = getattr(importlib.import_module(mod_name), cls_name)
+        setattr(cls, name, orig)
+        del _saved_methods[(mod_name, cls_name, name)]
     for (mod_name, name), orig in list(_saved.items()):
         mod = importlib.import_module(mod_name)
         setattr(mod, name, orig)

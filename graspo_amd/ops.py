@@ -156,6 +156,18 @@ def lse_finalize(state: torch.Tensor):
     return ops.lse_finalize(state, _stream(state))
 
 
+def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torch.Tensor,
+                  eos_token_id: int, pad_token_id: int, sequences: torch.Tensor | None,
+                  attention_mask: torch.Tensor | None, col: int, flags: torch.Tensor) -> None:
+    """After a sampler step: ``sequences[:, col] = ids``,
+    ``attention_mask[:, col] = ids != pad``, ``finished |= ids == eos`` (in
+    place) and ``flags = [rows still unfinished, rows with a bad status]``
+    (int32 [2]), in one launch."""
+    ops = load()
+    ops.decode_update(ids, status, finished, int(eos_token_id), int(pad_token_id), sequences,
+                      attention_mask, int(col), flags, _stream(ids))
+
+
 def new_lse_state(rows: int, device) -> torch.Tensor:
     return torch.empty((rows, 4), dtype=torch.float32, device=device)
 

@@ -241,6 +241,35 @@ int gtp_graspo_loss_backward(const float* logp, const float* old_logp,
                              int64_t B, int64_t T, float clip_lo,
                              float clip_hi, float* grad_logp, void* stream);
 
+/*
+ * gtp_decode_update_rows -- the generation loop's per-token bookkeeping after
+ * gtp_sample_rows, in one launch and without a host synchronisation.
+ *
+ * Replaces the statements that follow the sampler in the decode loops
+ *   src/graspo/backends/graspoflow/models/qwen3/adapter.py:292-305
+ *   src/graspo/backends/graspoflow/models/qwen35_36/generation.py:258-275,
+ *   :310-319, :558-575, :624-635
+ * (sequences = cat([sequences, next_token]); finished |= next_token == eos;
+ * all_finished = bool(finished.all()); attention_mask = sequences.ne(pad)).
+ *
+ *   ids       [B] int64, the sampler's out_ids (rows finished before the
+ *             step already hold pad_token_id)
+ *   status    [B] int32, the sampler's out_status, or NULL
+ *   finished  [B] uint8 (or bool) in/out: finished[b] |= ids[b] == eos_token_id
+ *   seq       [B, seq_stride] int64 or NULL: seq[b, col] = ids[b]
+ *   attn      [B, attn_stride] uint8 (or bool) or NULL:
+ *             attn[b, col] = ids[b] != pad_token_id
+ *   flags     [2] int32 out: rows not finished after the update, and rows
+ *             whose status is not GTP_ROW_OK.  The caller copies them to
+ *             host memory asynchronously; flags[0] == 0 is the reference's
+ *             all_finished.
+ */
+int gtp_decode_update_rows(const int64_t* ids, const int32_t* status, int64_t B,
+                           int64_t eos_token_id, int64_t pad_token_id,
+                           uint8_t* finished, int64_t* seq, int64_t seq_stride,
+                           uint8_t* attn, int64_t attn_stride, int64_t col,
+                           int32_t* flags, void* stream);
+
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
 

@@ -129,3 +129,42 @@ def test_graspo_loss_known_answer():
     row0 = -math.exp(0.1)
     row1 = (0.5 * math.exp(0.1) + 0.5 * math.exp(0.2)) / 2
     assert abs(float(got) - (row0 + row1) / 2) < 1e-6
+
+
+def test_integration_rebinds_decode_loop_methods(monkeypatch):
+    """install() replaces the adapters' decode-loop methods on their classes
+    (subclasses inherit them) and uninstall() restores the originals."""
+    import sys
+    import types
+
+    from graspo_amd import decode_loop
+
+    mods = {}
+    for mod_name, classes in integration.METHOD_TARGETS.items():
+        m = types.ModuleType(mod_name)
+        for cls_name, names in classes.items():
+            cls = type(cls_name, (), {n: (lambda self, **kw: "reference") for n in names})
+            setattr(m, cls_name, cls)
+        monkeypatch.setitem(sys.modules, mod_name, m)
+        mods[mod_name] = m
+    done = integration.install(targets={})
+    adapter_cls = mods["graspo.backends.graspoflow.models.qwen3.adapter"].Qwen3Adapter
+    assert adapter_cls._generate_group_with_kv_cache is decode_loop.generate_group_with_kv_cache
+    mixin = mods["graspo.backends.graspoflow.models.qwen35_36.generation"]._Qwen35GenerationMethods
+    sub = type("Qwen35Adapter", (mixin,), {})
+    assert sub._generate_multimodal_full_forward is decode_loop.generate_multimodal_full_forward
+    assert len(done) == 6
+    integration.uninstall()
+    assert adapter_cls._generate_group_with_kv_cache(None) == "reference"
+    assert sub._generate_multimodal_full_forward(None) == "reference"
+
+
+def test_decode_loop_has_no_cpu_path():
+    from graspo_amd.decode_loop import DecodeState
+
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        DecodeState(torch.zeros(2, 3, dtype=torch.int64), torch.zeros(2, dtype=torch.bool), 1, 0, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        graspo_amd.load().decode_update(torch.zeros(2, dtype=torch.int64), None,
+                                        torch.zeros(2, dtype=torch.bool), 1, 0, None, None, 0,
+                                        torch.zeros(2, dtype=torch.int32), 0)

@@ -124,6 +124,31 @@ def test_status_rows_and_padding():
     assert_parity(gpu_sample(x, **kw), oracle_sample(x, **kw))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("params", [dict(temperature=0.0), dict(temperature=1.0, top_k=5),
+                                    dict(temperature=1.0, top_p=0.9),
+                                    dict(temperature=0.7, top_k=300, top_p=0.9)])
+def test_rows_without_a_finite_value(dtype, params):
+    """Rows of NaN only, NaN with -inf only, and -inf only (no finite value
+    anywhere): non-finite for the first two and empty for the last, on every
+    kernel the call routes to (a NaN sum must survive merges of partial
+    log-sum-exps whose maxima are all -inf)."""
+    V = 1000
+    x = torch.randn(6, V)
+    x[0] = float("nan")
+    x[1] = float("-inf")
+    x[1, ::3] = float("nan")
+    x[2] = float("-inf")
+    x[3, 17] = float("nan")
+    x[4] = float("-inf")
+    x[4, 999] = 2.0
+    x = x.to(dtype)
+    kw = dict(params, uniforms=torch.full((6,), 0.25))
+    g = gpu_sample(x, **kw)
+    assert g.status.tolist()[:4] == [1, 1, 2, 1], (dtype, params, g.status)
+    assert_parity(g, oracle_sample(x, **kw), f"{dtype} {params}")
+
+
 @pytest.mark.parametrize("top_k", [0, 1, 7, 256, 257, 5000])
 def test_heavy_ties(top_k):
     """Uniform and few-valued rows: ties resolve by id (radix fallback when
