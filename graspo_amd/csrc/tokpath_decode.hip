@@ -7,8 +7,8 @@
 //   finished |= next_token.eq(eos_token_id)
 //   all_finished = bool(finished.all())          (a host sync every token)
 //   attention_mask = sequences.ne(pad_token_id)
-// (src/graspo/backends/graspoflow/models/qwen3/adapter.py:292-305,
-//  models/qwen35_36/generation.py:258-275).  Here one workgroup writes the
+// (src/graspo/backends/graspoflow/models/qwen3/adapter.py:293-304,
+//  models/qwen35_36/generation.py:259-270).  Here one workgroup writes the
 // token into a preallocated sequence column and the attention-mask column,
 // updates `finished` in place and writes two counters (rows still
 // unfinished, rows whose sampler status is not OK) that the host reads

@@ -246,9 +246,9 @@ int gtp_graspo_loss_backward(const float* logp, const float* old_logp,
  * gtp_sample_rows, in one launch and without a host synchronisation.
  *
  * Replaces the statements that follow the sampler in the decode loops
- *   src/graspo/backends/graspoflow/models/qwen3/adapter.py:292-305
- *   src/graspo/backends/graspoflow/models/qwen35_36/generation.py:258-275,
- *   :310-319, :558-575, :624-635
+ *   src/graspo/backends/graspoflow/models/qwen3/adapter.py:293-304, :338-351
+ *   src/graspo/backends/graspoflow/models/qwen35_36/generation.py:259-270,
+ *   :304-317, :558-569, :606-630
  * (sequences = cat([sequences, next_token]); finished |= next_token == eos;
  * all_finished = bool(finished.all()); attention_mask = sequences.ne(pad)).
  *
