@@ -173,12 +173,7 @@ struct Proc {
 // Exclusive prefix sum over the threads of the block (in thread order).
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  uint32_t incl = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t w = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += w;
-  }
+  const uint32_t incl = wave_scan_u32(v);  // DPP, no LDS round trip
   __syncthreads();
   if (lane == kWave - 1) red[wid] = incl;
   __syncthreads();
@@ -205,12 +200,7 @@ __device__ __forceinline__ void find_bucket(FastSmem& sm, uint32_t target) {
     c[q] = sm.hist[255 - 4 * lane - q];
     tot += c[q];
   }
-  uint32_t incl = tot;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t w = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += w;
-  }
+  const uint32_t incl = wave_scan_u32(tot);
   uint32_t above = incl - tot;
   if (above <= target && target < incl) {
 #pragma unroll
@@ -237,12 +227,7 @@ __device__ __forceinline__ int32_t wave_find_bucket(const uint32_t* h, uint32_t 
   uint32_t tot = 0;
 #pragma unroll 8
   for (int q = 0; q < PL; ++q) tot += hl[q];
-  uint32_t incl = tot;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t w = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += w;
-  }
+  const uint32_t incl = wave_scan_u32(tot);
   const bool here = incl - tot <= target && target < incl;
   const unsigned long long who = __ballot(here);
   if (!who) return -1;
@@ -262,8 +247,8 @@ __device__ __forceinline__ int32_t wave_find_bucket(const uint32_t* h, uint32_t 
       above += cq;
     }
   }
-  if (above_out) *above_out = (uint32_t)__shfl((int)ab, src, kWave);
-  return __shfl(bin, src, kWave);
+  if (above_out) *above_out = (uint32_t)__builtin_amdgcn_readlane((int)ab, src);
+  return __builtin_amdgcn_readlane(bin, src);
 }
 
 // Sort the 64 R values of a wave in descending order in registers (bitonic
@@ -573,11 +558,11 @@ __device__ __forceinline__ void select_top_slow(FastSmem& sm, const Slice<T>& c,
 // the weights of ranks r); the cut and the draw are counts of prefix sums
 // below a bound, taken with ballots.  Callers sync before (lists complete).
 __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& fa, int64_t b,
-                                           float lm, float ls, bool bad_hist, uint32_t nk) {
+                                           float u, float lm, float ls, bool bad_hist,
+                                           uint32_t nk) {
   const SamplerArgs& a = fa.a;
   const int lane = threadIdx.x;
   if (lane >= kWave) return;
-  const float u = fa.greedy ? 0.0f : a.uniforms[b];
   // logprob = x - m - ln s, rounded once (raw_logprob)
   const float lse_m = lm, lse_ln = __builtin_amdgcn_logf(ls) * kLn2;
   int32_t status = GTP_ROW_OK;
@@ -609,11 +594,14 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   const uint32_t r0 = 2u * (uint32_t)lane, r1 = r0 + 1u;
   const unsigned long long w0 = r0 < nk ? detexp_fix(rank_key_y(sm.fkey[r0]) - m) : 0ull;
   const unsigned long long w1 = r1 < nk ? detexp_fix(rank_key_y(sm.fkey[r1]) - m) : 0ull;
-  const unsigned long long i1 = wave_incl_scan_u64(w0 + w1);
+  const unsigned long long i1 = wave_scan_u64(w0 + w1);
   const unsigned long long i0 = i1 - w1;
   auto incl_at = [&](uint32_t r) -> unsigned long long {  // r wave-uniform
     const unsigned long long v = (r & 1u) ? i1 : i0;
-    return __shfl(v, (int)(r >> 1), kWave);
+    const int l = (int)(r >> 1);
+    return ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l)
+            << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
   };
   auto count_le = [&](uint32_t lim, unsigned long long bound) -> uint32_t {  // #{r < lim : incl[r] <= bound}
     const unsigned long long c0 = __ballot(r0 < lim && i0 <= bound);
@@ -636,7 +624,8 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
 
 // The last workgroup of a split row: gather the S sorted lists, rank the
 // union by binary search, finish.  Block-uniform.
-__device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int64_t b, int S) {
+__device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int64_t b, float u,
+                                          int S) {
   const int tid = threadIdx.x;
   const uint32_t Kc = (uint32_t)fa.Kc;
   const unsigned char* slots = fa.ws + fa.cnt_bytes + (size_t)b * S * kSlotBytes;
@@ -699,7 +688,7 @@ __device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int6
     }
   }
   __syncthreads();
-  finish_row(sm, fa, b, lm, ls, any_bad_hist, nk);
+  finish_row(sm, fa, b, u, lm, ls, any_bad_hist, nk);
 }
 
 // --------------------------------------------------------------- the kernel
@@ -733,23 +722,19 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   const bool read_hist = a.hist && a.hist_len > 0 && (fa.use_pen || s == 0);
   const int32_t* hrow = a.hist + b * a.hist_stride;
 
-  // ---- 0. counters, histograms and penalty bitmap cleared, first batch of
-  // history ids requested
+  // ---- 0. the first global requests go out before anything else: the first
+  // batch of history ids here, the pilot vectors in the stream; then (the
+  // stream's prologue) counters, histograms and penalty bitmap are cleared
   const int lane = tid & (kWave - 1);
-  if (tid == 0) {
-    sm.chunk_ctr = 0u;
-    sm.pool_n = 0u;
-    sm.kmax16 = 0u;
-    sm.bucket = -1;
-    sm.parrive = 0u;
-    sm.theta_ready = 0u;
+  // the row's uniform, needed only by the finish: requested first, so that no
+  // global load sits on the path after the stream
+  const float u_row = fa.greedy ? 0.0f : a.uniforms[b];
+  int32_t hv[kHistPer];
+#pragma unroll
+  for (int q = 0; q < kHistPer; ++q) {
+    const int64_t j = tid + (int64_t)q * kFT;
+    hv[q] = read_hist && j < a.hist_len ? hrow[j] : -1;
   }
-  for (int i = tid; i < kPHist; i += kFT) sm.phist[i] = 0u;
-  if (fa.use_pen)
-    for (int i = tid; i < nw; i += kFT) sm.pen[i] = 0u;
-  __syncthreads();
-  // history ids past the first kHistPer x 1024 (long histories only): set
-  // their bits now, before the stream's loads are in flight
   bool bad_hist = false;
   auto hist_bits = [&](int32_t id) {
     if (id >= a.V)
@@ -757,15 +742,23 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     else if (fa.use_pen && id >= e0 && id < e1)
       atomicOr(&sm.pen[(uint32_t)(id >> 5) - c.w0], 1u << (id & 31));
   };
-  if (read_hist)
-    for (int64_t j = (int64_t)kHistPer * kFT + tid; j < a.hist_len; j += kFT) hist_bits(hrow[j]);
-  // the first batch: requested now, used by the pilot
-  int32_t hv[kHistPer];
-#pragma unroll
-  for (int q = 0; q < kHistPer; ++q) {
-    const int64_t j = tid + (int64_t)q * kFT;
-    hv[q] = read_hist && j < a.hist_len ? hrow[j] : -1;
-  }
+  auto prologue = [&]() {
+    if (tid == 0) {
+      sm.chunk_ctr = 0u;
+      sm.pool_n = 0u;
+      sm.kmax16 = 0u;
+      sm.bucket = -1;
+      sm.parrive = 0u;
+      sm.theta_ready = 0u;
+    }
+    for (int i = tid; i < kPHist; i += kFT) sm.phist[i] = 0u;
+    if (fa.use_pen)
+      for (int i = tid; i < nw; i += kFT) sm.pen[i] = 0u;
+    __syncthreads();
+    // history ids past the first kHistPer x 1024 (long histories only)
+    if (read_hist)
+      for (int64_t j = (int64_t)kHistPer * kFT + tid; j < a.hist_len; j += kFT) hist_bits(hrow[j]);
+  };
 
   // ---- 1. stream with a prefix pilot.
   // Every token of the slice is folded into the raw log-sum-exp (the logprob
@@ -825,7 +818,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     wave_sort_desc(v);
     const uint32_t r = (Kc - 1u) / kWave, l = (Kc - 1u) % kWave;
     const uint32_t vr = r == 0 ? v[0] : v[1];  // Kc <= 128 <= 64 R
-    return (uint32_t)__shfl((int)vr, (int)l, kWave);
+    return (uint32_t)__builtin_amdgcn_readlane((int)vr, (int)l);
   };
   // the thread's pilot key and the wave's arrival; the last wave to arrive
   // turns the 1024 keys into the threshold (no block barrier: waves that
@@ -851,11 +844,15 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     wave_sort_desc<1>(k16);
     if (lane < kWTop) sm.wtop[(tid / kWave) * kWTop + lane] = k16[0];
     uint32_t arrived = 0;
-    if (lane == 0) arrived = atomicAdd(&sm.parrive, 1u);
+    if (lane == 0)
+      arrived = __hip_atomic_fetch_add(&sm.parrive, 1u, __ATOMIC_ACQ_REL,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(arrived) != (uint32_t)kFWaves - 1u) return;
     // last wave: theta1 = the Kc-th largest of the posted keys.  They are
     // keys of distinct threads, so at least Kc threads reach it (exact
-    // unless one wave held more than 16 of the Kc largest).
+    // unless one wave held more than 16 of the Kc largest).  (Taking theta
+    // from the first waves to post instead makes it ready ~2 us earlier but
+    // doubles the pool, and with a penalty and no mask overflows it.)
     uint32_t t16;
     if (Kc <= (uint32_t)kWave) {
       uint32_t v[2];  // the 8 largest keys of each wave suffice
@@ -958,7 +955,9 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     for (int k = 0; k < kFG; ++k) {
       // this vector's allow bits: bit (o*E) & 31 of the chunk's word o*E >> 5
       // (o = its offset in the chunk), held by that lane; with a mask the
-      // hit test uses the largest allowed value
+      // hit test uses the largest allowed value (a test on the raw maximum
+      // queues about ten times as many vectors, and their drains cost more
+      // than this)
       uint32_t ab = (1u << E) - 1u;
       float gh = gm[k];
       if (kMask) {
@@ -984,7 +983,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   };
   // non-temporal: the row is read once
   stream_vectors_prefix<T, kFT, kNP, kFG, true, kMask>(c.row, c.v0, c.v1, c.mrow, &sm.chunk_ctr,
-                                                    pre, post, fold);
+                                                    prologue, pre, post, fold);
   if (qn) drain(qn);
   // tokens past the last whole vector (last slice only)
   for (int64_t id = c.tail0 + tid; id < a.V; id += kFT) {
@@ -1254,7 +1253,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   }
   __syncthreads();
   if (S == 1) {
-    finish_row(sm, fa, b, lm, ls, bad_hist, nout);
+    finish_row(sm, fa, b, u_row, lm, ls, bad_hist, nout);
     return;
   }
   if (tid == 0) {
@@ -1285,7 +1284,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   }
   __syncthreads();
   if (!sm.flag) return;
-  merge_row(sm, fa, b, S);
+  merge_row(sm, fa, b, u_row, S);
 }
 
 // ------------------------------------------------------------------ planning

@@ -512,8 +512,10 @@ __device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, in
 // Stream vectors [v0, v1) (v1 > v0) of a 16-byte aligned row with a prefix
 // pilot.  Thread t loads the pilot vectors v0 + q*NT + t (q < NP, inside the
 // range; np = number of pilot vectors, entries at or past np re-read the
-// first vector) and calls `pre(p, sp, np)` on them before any other load is
-// issued; then the wave's first two chunks of the rest are issued and
+// first vector), then calls `prologue()` (block-wide set-up, which may hold a
+// barrier: the pilot loads are already in flight) and `pre(p, sp, np)` on
+// them before any other load is issued; then the wave's first two chunks of
+// the rest are issued and
 // `post(p, sp, np)` runs with them in flight.  `pre` must not hold block
 // barriers: a wave that waits on another before issuing its own loads lets
 // the memory pipeline drain.  The rest of the range is streamed as in
@@ -527,12 +529,12 @@ __device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, in
 // one).  Every load before the pilot is unconditional (out-of-range ones
 // re-read the first vector), so the compiler can wait for the pilot data
 // alone.
-template <typename T, int NT, int NP, int NG, bool kNonTemporal, bool kSide, typename Pre,
-          typename Post, typename Fold>
+template <typename T, int NT, int NP, int NG, bool kNonTemporal, bool kSide, typename Prologue,
+          typename Pre, typename Post, typename Fold>
 __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row, int64_t v0,
                                                       int64_t v1, const uint32_t* __restrict__ side,
-                                                      uint32_t* counter, Pre&& pre, Post&& post,
-                                                      Fold&& fold) {
+                                                      uint32_t* counter, Prologue&& prologue,
+                                                      Pre&& pre, Post&& post, Fold&& fold) {
   constexpr int E = Vec<T>::kE;
   constexpr uint32_t kChunk = (uint32_t)kWave * NG;
   const int64_t n = v1 - v0 > 0 ? v1 - v0 : 0;
@@ -550,6 +552,7 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
     p[q] = kNonTemporal ? __builtin_nontemporal_load(a) : *a;
     sp[q] = kSide ? side[((uint64_t)(v0 + vi) * E) >> 5] : 0xFFFFFFFFu;
   }
+  prologue();  // block-wide set-up (its barrier included) while the pilot loads fly
   pre(p, sp, np);
   // the rest: [v0 + np, v1) in per-wave chunks (an empty rest re-reads the
   // first vector of the range)
