@@ -23,6 +23,10 @@ the reference's torch expression over [16, 2048] token logprobs.
 [256, 248320] bf16 shape: the decode-loop drop-in against the reference's
 loop body, both on this library's sampler, with a stand-in model.
 
+``hidden_logprobs`` times the hidden-state logprob path (8192 tokens, hidden
+4096, vocabulary 248320) as the callers use it, against the reference's fp32
+expression, with the bf16 GEMM's TFLOP/s against the matrix-core peak.
+
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
 [64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
 512 MB buffer written between launches to evict the MALL.
@@ -189,6 +193,70 @@ def time_graspo_loss(dev, B: int = 16, T: int = 2048, iters: int = 50):
     out["shape"] = [B, T]
     out["what"] = "forward + backward per call, HIP events around 50 back-to-back calls"
     return out
+
+
+def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
+    """The hidden-state logprob path at N tokens x H x V (tensor_utils.py:
+    167-186 with the callers' fp32 copies of bf16 hidden states and lm_head,
+    qwen3/model.py:361-365): the drop-in (exact bf16 narrowing, bf16
+    matrix-core chunk GEMMs with fp32 logits, the lse kernel) against the
+    reference's expression in fp32 on the same device, plus the bf16 GEMM
+    alone over the same chunks (fp32 output), whose TFLOP/s are reported
+    against the 2.5 PFLOP/s dense bf16 peak."""
+    import torch
+    import torch.nn.functional as F
+
+    from graspo_amd import tensor_utils as TU
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    h = torch.randn(N, H, device=dev, generator=g).to(torch.bfloat16).float()
+    w = (torch.randn(V, H, device=dev, generator=g) * 0.02).to(torch.bfloat16).float()
+    ids = torch.randint(0, V, (N,), device=dev, generator=g)
+    chunk = 32768
+
+    def reference():
+        sel = (h * w.index_select(0, ids)).sum(dim=-1)
+        lse = None
+        for start in range(0, V, chunk):
+            c = torch.logsumexp(F.linear(h, w[start:start + chunk]), dim=-1)
+            lse = c if lse is None else torch.logaddexp(lse, c)
+        return sel - lse
+
+    def dropin():
+        return TU._selected_token_log_probs_from_hidden(h, w, ids)
+
+    hb, wb = h.to(torch.bfloat16), w.to(torch.bfloat16)
+
+    def gemm_only():
+        for start in range(0, V, chunk):
+            torch.mm(hb, wb[start:start + chunk].t(), out_dtype=torch.float32)
+
+    def clock(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            out = fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps, out
+
+    ours_ms, lp = clock(dropin, 5)
+    gemm_ms, _ = clock(gemm_only, 5)
+    ref_ms, lp_ref = clock(reference, 2)
+    flops = 2.0 * N * H * V
+    return {
+        "shape": {"tokens": N, "hidden": H, "vocab": V, "chunk": chunk},
+        "dropin_ms": round(ours_ms, 3), "reference_fp32_ms": round(ref_ms, 3),
+        "gemm_bf16_ms": round(gemm_ms, 3),
+        "gemm_tflops": round(flops / (gemm_ms * 1e-3) / 1e12, 1),
+        "gemm_frac_bf16_peak": round(flops / (gemm_ms * 1e-3) / 2.5e15, 4),
+        "dropin_tflops": round(flops / (ours_ms * 1e-3) / 1e12, 1),
+        "max_abs_diff_vs_reference": round(float((lp - lp_ref).abs().max()), 7),
+        "what": "fp32 inputs holding bf16 values, as the callers pass them; HIP events, "
+                "5 (drop-in, GEMM) and 2 (reference) calls after one warm-up",
+    }
 
 
 def time_decode_loop(dev, B: int = 256, V: int = 248320, steps: int = 24):
@@ -377,6 +445,7 @@ def main() -> int:
     del lx, lt, batches, wl_b, grad, g_lp, lse, lp_f
     line["graspo_loss"] = time_graspo_loss(dev)
     line["decode_loop"] = time_decode_loop(dev)
+    line["hidden_logprobs"] = time_hidden_logprobs(dev)
     if not args.no_per_config:
         flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
         line["per_config"] = {

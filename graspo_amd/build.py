@@ -24,7 +24,8 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 EXT_NAME = "_graspo_tokpath_ops"
 
 HIP_SOURCES = ["tokpath_logprob.hip", "tokpath_sampler.hip", "tokpath_sampler_fast.hip",
-               "tokpath_loss.hip", "tokpath_decode.hip"]
+               "tokpath_loss.hip", "tokpath_decode.hip",
+               "tokpath_narrow.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

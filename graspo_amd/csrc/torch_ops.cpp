@@ -1,7 +1,7 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
-// lse_finalize, decode_update}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lse_finalize, decode_update, to_bf16_exact}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -375,6 +375,22 @@ void decode_update(const at::Tensor& ids, const c10::optional<at::Tensor>& statu
   check_rc(rc, "gtp_decode_update_rows");
 }
 
+// bf16 copy of a contiguous fp32 tensor, and whether any value was not a bf16
+// value (a device flag the caller reads)
+std::tuple<at::Tensor, at::Tensor> to_bf16_exact(const at::Tensor& src, int64_t stream) {
+  TORCH_CHECK(src.is_cuda(), "graspo_tokpath.to_bf16_exact: src must be a GPU tensor");
+  TORCH_CHECK(src.scalar_type() == at::kFloat && src.is_contiguous(),
+              "graspo_tokpath.to_bf16_exact: src must be a contiguous float32 tensor");
+  at::Tensor dst = at::empty(src.sizes(), src.options().dtype(at::kBFloat16));
+  at::Tensor flag = at::zeros({1}, src.options().dtype(at::kInt));
+  const int rc = gtp_f32_to_bf16_exact(src.data_ptr<float>(), src.numel(),
+                                       static_cast<uint16_t*>(dst.data_ptr()),
+                                       reinterpret_cast<uint32_t*>(flag.data_ptr<int32_t>()),
+                                       reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_f32_to_bf16_exact");
+  return {dst, flag};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(graspo_tokpath, m) {
@@ -408,4 +424,5 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "int pad_token_id, Tensor(b!)? sequences, Tensor(c!)? attention_mask, int col, "
       "Tensor(d!) flags, int stream) -> ()",
       &decode_update);
+  m.def("to_bf16_exact(Tensor src, int stream) -> (Tensor, Tensor)", &to_bf16_exact);
 }

@@ -168,6 +168,14 @@ def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torc
                       attention_mask, int(col), flags, _stream(ids))
 
 
+def to_bf16_exact(src: torch.Tensor):
+    """(bf16 copy, inexact) of a contiguous fp32 GPU tensor: the copy holds the
+    upper 16 bits of each value, and ``inexact`` (int32 [1], on the device) is
+    nonzero when some value is not a bf16 value."""
+    ops = load()
+    return ops.to_bf16_exact(src.contiguous(), _stream(src))
+
+
 def new_lse_state(rows: int, device) -> torch.Tensor:
     return torch.empty((rows, 4), dtype=torch.float32, device=device)
 

@@ -87,9 +87,39 @@ def _broadcast_and_pad_finished(
 
 # ------------------------------------------------------------- logprobs
 
+def _matrix_core_operands(h2: torch.Tensor, weight: torch.Tensor):
+    """bf16 operands for the chunk GEMMs, or None to multiply in the inputs'
+    own dtype.
+
+    bf16 / fp16 inputs are used as they are.  fp32 inputs -- the reference's
+    callers pass ``hidden.float()`` and ``lm_head.weight.float()``, fp32
+    copies of bf16 tensors -- are narrowed to bf16 in one pass that also
+    reports whether every value is a bf16 value (one host synchronisation).
+    When it is, a bf16 x bf16 product is exact in fp32, so a matrix-core GEMM
+    with fp32 output computes the same products as the reference's fp32 GEMM
+    (only the summation order differs); otherwise the fp32 GEMM is kept."""
+    if h2.dtype in (torch.bfloat16, torch.float16) and weight.dtype == h2.dtype:
+        return h2, weight
+    if h2.dtype == torch.float32 and weight.dtype == torch.float32 and h2.is_cuda:
+        hb, fh = ops.to_bf16_exact(h2)
+        wb, fw = ops.to_bf16_exact(weight)
+        if int((fh | fw).item()) == 0:
+            return hb, wb
+    return None
+
+
+def _chunk_logits(h2, weight, mc, start, chunk):
+    """fp32 logits of vocabulary columns [start, start + chunk)."""
+    if mc is not None:
+        hb, wb = mc
+        return torch.mm(hb, wb[start : start + chunk].t(), out_dtype=torch.float32)
+    return F.linear(h2, weight[start : start + chunk]).float()
+
+
 class _SelectedLogProbsFromHidden(torch.autograd.Function):
     """log_softmax(h W^T)[target] without materialising [N, V] logits:
-    vocabulary chunks of the GEMM are folded into a running (m, s) state by
+    vocabulary chunks of the GEMM (bf16 matrix cores with fp32 output when
+    the operands are bf16 values) are folded into a running (m, s) state by
     the lse kernel; the backward recomputes each chunk's softmax."""
 
     @staticmethod
@@ -98,20 +128,25 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         h2 = hidden.reshape(-1, H)
         t = output_ids.reshape(-1)
         N, V = h2.shape[0], weight.shape[0]
+        mc = _matrix_core_operands(h2, weight)
         state = ops.new_lse_state(N, hidden.device)
         for c, start in enumerate(range(0, V, chunk)):
-            logits = F.linear(h2, weight[start : start + chunk])
+            logits = _chunk_logits(h2, weight, mc, start, chunk)
             ops.lse_partial(logits, t, start, state, accumulate=c > 0)
         lp, _ = ops.lse_finalize(state)
         lse = state[:, 0] + torch.log(state[:, 1])
-        ctx.save_for_backward(h2, weight, t, lse)
+        saved = (h2, weight, t, lse) + (mc if mc is not None else ())
+        ctx.save_for_backward(*saved)
+        ctx.has_mc = mc is not None
         ctx.chunk = chunk
         ctx.out_shape = output_ids.shape
         return lp.view(output_ids.shape)
 
     @staticmethod
     def backward(ctx, grad_out):
-        h2, weight, t, lse = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        h2, weight, t, lse = saved[:4]
+        mc = saved[4:6] if ctx.has_mc else None
         g = grad_out.reshape(-1).to(torch.float32)
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         grad_h = torch.zeros_like(h2) if need_h else None
@@ -119,7 +154,8 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         for start in range(0, weight.shape[0], ctx.chunk):
             w_c = weight[start : start + ctx.chunk]
             # g * (onehot - softmax) of this chunk's logits, one kernel pass
-            gc = ops.logprob_backward(F.linear(h2, w_c), t, g, lse, col_offset=start)
+            logits = _chunk_logits(h2, weight, mc, start, ctx.chunk)
+            gc = ops.logprob_backward(logits, t, g, lse, col_offset=start)
             if need_h:
                 grad_h += gc.to(h2.dtype) @ w_c.to(h2.dtype)
             if need_w:
@@ -138,9 +174,11 @@ def _selected_token_log_probs_from_hidden(
 ) -> torch.Tensor:
     """logit[target] - logsumexp over the vocabulary, fp32 [*output_ids.shape]
     (reference: tensor_utils.py:167-186).  The chunk loop keeps the
-    reference's ``vocab_chunk_size`` GEMMs; the logsumexp / logaddexp fold is
-    the lse kernel.  Differentiable in ``hidden_states`` and
-    ``lm_head_weight``."""
+    reference's ``vocab_chunk_size`` GEMMs -- on bf16 matrix cores with fp32
+    logits when the operands are bf16 values, as the reference's ``.float()``
+    copies are -- and the logsumexp / logaddexp fold is the lse kernel.
+    Differentiable in ``hidden_states`` and ``lm_head_weight`` (the gradient
+    GEMMs stay in the operands' dtype)."""
     return _SelectedLogProbsFromHidden.apply(
         hidden_states, lm_head_weight, output_ids, int(vocab_chunk_size)
     )

@@ -270,6 +270,21 @@ int gtp_decode_update_rows(const int64_t* ids, const int32_t* status, int64_t B,
                            uint8_t* attn, int64_t attn_stride, int64_t col,
                            int32_t* flags, void* stream);
 
+/*
+ * gtp_f32_to_bf16_exact -- dst[i] = the upper 16 bits of src[i] (the bf16
+ * value of an fp32 value that is one), for n elements; *inexact |= 1 when any
+ * src[i] has nonzero lower 16 bits (it is not a bf16 value, and dst[i] is
+ * then not its rounding).  The caller zeroes *inexact.  One HBM pass.
+ *
+ * Serves the hidden-state logprob path: the reference hands
+ * _selected_token_log_probs_from_hidden (tensor_utils.py:167-186) fp32 copies
+ * of bf16 tensors (qwen3/model.py:361-365, qwen35_36/training.py:619-623) and
+ * multiplies them in fp32; when both operands are bf16 values the chunk GEMMs
+ * run on bf16 matrix cores with fp32 output instead, with the same products.
+ */
+int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
+                          uint32_t* inexact, void* stream);
+
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
 

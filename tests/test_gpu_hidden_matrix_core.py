@@ -1,0 +1,106 @@
+"""The hidden-state logprob path's matrix-core route.
+
+``gtp_f32_to_bf16_exact`` must return the upper 16 bits of every fp32 value
+and flag exactly the inputs that are not bf16 values (nonzero lower bits,
+NaN payloads there included), for aligned, unaligned and ragged lengths.
+
+``_selected_token_log_probs_from_hidden`` must take the bf16 route when its
+fp32 operands are bf16 values (as the reference's ``.float()`` copies are),
+stay in fp32 otherwise, and in every case agree with an fp64 evaluation of
+the reference expression (tensor_utils.py:167-186) within 1e-4 -- well inside
+the 1e-3 contract, since the bf16 x bf16 products are exact in fp32 and the
+logits are kept in fp32."""
+
+import pytest
+import torch
+
+from graspo_amd import ops
+from graspo_amd import tensor_utils as TU
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1000, 4099, 1 << 20])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_narrowing_matches_truncation_and_flags(n, offset):
+    g = torch.Generator().manual_seed(n + offset)
+    exact = torch.randn(n + offset, generator=g).to(torch.bfloat16).float()
+    src = exact.to(DEV)[offset:]  # offset 1: a 4-byte aligned, not 16-byte aligned start
+    bf, flag = ops.to_bf16_exact(src)
+    torch.cuda.synchronize()
+    assert int(flag) == 0
+    assert torch.equal(bf.cpu().view(torch.int16), exact[offset:].to(torch.bfloat16).view(torch.int16))
+    for pos in {0, n // 2, n - 1}:
+        bad = exact.clone()
+        bits = bad.view(torch.int32)
+        bits[offset + pos] |= 1  # one low bit: not a bf16 value
+        _, flag = ops.to_bf16_exact(bad.to(DEV)[offset:])
+        torch.cuda.synchronize()
+        assert int(flag) == 1, (n, offset, pos)
+
+
+def test_narrowing_specials():
+    vals = torch.tensor([0.0, -0.0, float("inf"), float("-inf"), float("nan"), 1e-40, -3.5])
+    bf, flag = ops.to_bf16_exact(vals.to(DEV))
+    torch.cuda.synchronize()
+    assert int(flag) == 1  # 1e-40 (a subnormal) has low bits
+    head = vals[:6].clone()
+    head[5] = 2.0 ** -126
+    bf, flag = ops.to_bf16_exact(head.to(DEV))
+    torch.cuda.synchronize()
+    assert int(flag) == 0
+    upper = (head.view(torch.int32) >> 16).to(torch.int16)  # the contract: the upper 16 bits
+    assert torch.equal(bf.cpu().view(torch.int16), upper)
+    payload = torch.tensor([0x7F800001], dtype=torch.int32).view(torch.float32)  # NaN, low payload
+    _, flag = ops.to_bf16_exact(payload.to(DEV))
+    torch.cuda.synchronize()
+    assert int(flag) == 1
+
+
+def _reference_fp64(h, w, ids):
+    logits = h.double() @ w.double().t()
+    return logits.gather(-1, ids.unsqueeze(-1)).squeeze(-1) - torch.logsumexp(logits, -1)
+
+
+@pytest.mark.parametrize("kind", ["fp32_of_bf16", "fp32_inexact", "bf16"])
+def test_hidden_path_routes_and_accuracy(kind):
+    g = torch.Generator().manual_seed(7)
+    B, S, H, V = 2, 33, 256, 20000
+    h = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    w = (torch.randn(V, H, generator=g) * 0.15).to(torch.bfloat16)
+    ids = torch.randint(0, V, (B, S), generator=g)
+    if kind == "fp32_of_bf16":
+        h_in, w_in = h.float(), w.float()
+    elif kind == "fp32_inexact":
+        h_in, w_in = h.float(), w.float() + 1e-6 * torch.randn(V, H, generator=g)
+    else:
+        h_in, w_in = h, w
+    h_in, w_in, ids_d = h_in.to(DEV), w_in.to(DEV), ids.to(DEV)
+    mc = TU._matrix_core_operands(h_in.reshape(-1, H), w_in)
+    assert (mc is not None) == (kind != "fp32_inexact")
+    print("hidden route", kind, flush=True)
+    out = TU._selected_token_log_probs_from_hidden(h_in, w_in, ids_d, vocab_chunk_size=4096)
+    ref = _reference_fp64(h_in.cpu(), w_in.cpu(), ids)
+    err = float((out.double().cpu() - ref).abs().max())
+    assert err <= 1e-4, (kind, err)
+
+
+def test_hidden_path_gradients_on_the_bf16_route():
+    g = torch.Generator().manual_seed(8)
+    B, S, H, V = 2, 9, 64, 5000
+    h = torch.randn(B, S, H, generator=g).to(torch.bfloat16).float().to(DEV).requires_grad_(True)
+    w = (torch.randn(V, H, generator=g) * 0.2).to(torch.bfloat16).float().to(DEV)
+    w.requires_grad_(True)
+    ids = torch.randint(0, V, (B, S), generator=g).to(DEV)
+    out = TU._selected_token_log_probs_from_hidden(h, w, ids, vocab_chunk_size=1024)
+    gout = torch.randn(B, S, generator=g).to(DEV)
+    (out * gout).sum().backward()
+    h2 = h.detach().double().requires_grad_(True)
+    w2 = w.detach().double().requires_grad_(True)
+    logits = h2 @ w2.t()
+    ref = logits.gather(-1, ids.unsqueeze(-1)).squeeze(-1) - torch.logsumexp(logits, -1)
+    (ref * gout.double()).sum().backward()
+    assert float((out.double() - ref).abs().max()) <= 1e-4
+    assert float((h.grad.double() - h2.grad).abs().max()) <= 1e-4
+    assert float((w.grad.double() - w2.grad).abs().max()) <= 1e-4
