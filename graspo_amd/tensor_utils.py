@@ -130,6 +130,8 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         N, V = h2.shape[0], weight.shape[0]
         mc = _matrix_core_operands(h2, weight)
         state = ops.new_lse_state(N, hidden.device)
+        # (running each chunk's lse on a second stream beside the next GEMM
+        # was slower: 21.4 against 16.5 ms at 8192 x 4096 x 248320)
         for c, start in enumerate(range(0, V, chunk)):
             logits = _chunk_logits(h2, weight, mc, start, chunk)
             ops.lse_partial(logits, t, start, state, accumulate=c > 0)
