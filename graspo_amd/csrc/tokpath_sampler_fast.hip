@@ -932,7 +932,8 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     }
     qn = rest;
   };
-  auto fold = [&](float(&x)[kFG][E], const u32x4(&raw)[kFG], uint32_t sw, int64_t vbase,
+  auto fold = [&](float(&x)[kFG][E], const u32x4(&raw)[kFG], const uint32_t(&sw)[kFG],
+                  int64_t vbase,
                   bool last) {
     float gm[kFG];
 #pragma unroll
@@ -953,16 +954,14 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     lse_fold_block_max<false, kFG, E>(st, x, cm);
 #pragma unroll
     for (int k = 0; k < kFG; ++k) {
-      // this vector's allow bits: bit (o*E) & 31 of the chunk's word o*E >> 5
-      // (o = its offset in the chunk), held by that lane; with a mask the
-      // hit test uses the largest allowed value (a test on the raw maximum
-      // queues about ten times as many vectors, and their drains cost more
-      // than this)
+      // this vector's allow bits (its word came with its data); with a mask
+      // the hit test uses the largest allowed value (a test on the raw
+      // maximum queues about ten times as many vectors, and their drains
+      // cost more than this)
       uint32_t ab = (1u << E) - 1u;
       float gh = gm[k];
       if (kMask) {
-        const uint32_t o = (uint32_t)(k * kWave + lane) * E;
-        ab = ((uint32_t)__shfl((int)sw, (int)(o >> 5), kWave) >> (o & 31u)) & ((1u << E) - 1u);
+        ab = allow_bits(sw[k], vbase + (int64_t)k * kWave);
         float xm[E];
 #pragma unroll
         for (int j = 0; j < E; ++j) xm[j] = (ab >> j) & 1u ? x[k][j] : kNegInf;

@@ -522,11 +522,9 @@ __device__ __forceinline__ void stream_vectors_dyn(const T* __restrict__ row, in
 // stream_vectors_dyn: `fold(x, raw, sw, vec_index, last)`, vector k of the
 // block (raw 16 bytes raw[k], converted x[k]) at vec_index + k*64.
 // With kSide, `side` is a bit array with one bit per element (E bits per
-// vector, bit i of word i >> 5): pilot vector v brings sp[q] = the word
-// holding its bits, and with each chunk lane l brings sw = word l of the
-// chunk's bits (the chunk's first element must be 32-aligned in `side`,
-// i.e. v0 + np a multiple of 32 / E; words past the range re-read the last
-// one).  Every load before the pilot is unconditional (out-of-range ones
+// vector, bit i of word i >> 5): every vector, pilot or chunk, brings the
+// word holding its bits (sp[q] for the pilot, sw[k] for vector k of a
+// chunk).  Every load before the pilot is unconditional (out-of-range ones
 // re-read the first vector), so the compiler can wait for the pilot data
 // alone.
 template <typename T, int NT, int NP, int NG, bool kNonTemporal, bool kSide, typename Prologue,
@@ -565,11 +563,10 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
     if (lane == 0) c = atomicAdd(counter, 1u);
     return __builtin_amdgcn_readfirstlane(c);
   };
-  const uint64_t w_first = ((uint64_t)(v0 + (np < n ? np : 0)) * E) >> 5;
-  const uint64_t w_last = ((uint64_t)v1 * E - 1) >> 5;
+  const int64_t vfirst = v0 + (np < n ? np : 0);  // the vector at base2
   u32x4 a[NG], b[NG];
-  uint32_t swa = 0xFFFFFFFFu, swb = 0xFFFFFFFFu;
-  auto issue = [&](u32x4(&buf)[NG], uint32_t& sw, uint32_t chunk) {
+  uint32_t swa[NG], swb[NG];
+  auto issue = [&](u32x4(&buf)[NG], uint32_t(&sw)[NG], uint32_t chunk) {
     const bool live = chunk < nchunks;
     const uint32_t first = chunk * kChunk + lane;
 #pragma unroll
@@ -582,13 +579,13 @@ __device__ __forceinline__ void stream_vectors_prefix(const T* __restrict__ row,
         buf[k] = __builtin_nontemporal_load(q);
       else
         buf[k] = *q;
-    }
-    if (kSide) {
-      uint64_t w = w_first + (((uint64_t)(live ? chunk : 0u) * kChunk * E) >> 5) + lane;
-      sw = side[w < w_last ? w : w_last];
+      // the word holding this vector's bits, requested with its data (a
+      // shuffle from the lane that loaded it would put an LDS round trip on
+      // every vector's path)
+      sw[k] = kSide ? side[((uint64_t)(vfirst + vi) * E) >> 5] : 0xFFFFFFFFu;
     }
   };
-  auto consume = [&](const u32x4(&buf)[NG], uint32_t sw, uint32_t chunk) {
+  auto consume = [&](const u32x4(&buf)[NG], const uint32_t(&sw)[NG], uint32_t chunk) {
     float x[NG][E];
 #pragma unroll
     for (int k = 0; k < NG; ++k) Vec<T>::cvt(buf[k], x[k]);
