@@ -104,7 +104,7 @@ def install(targets: dict[str, tuple[str, ...]] | None = None, *, strict: bool =
                     _saved_methods[key] = cls.__dict__[name]
                 setattr(cls, name, METHOD_REPLACEMENTS[name])
                 done.append((mod_name, f"{cls_name}.{name}"))
-    for mod_name, names in (targets or TARGETS).items():
+    for mod_name, names in (TARGETS if targets is None else targets).items():
         try:
             mod = importlib.import_module(mod_name)
         except ImportError:
