@@ -245,6 +245,27 @@ def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
     ours_ms, lp = clock(dropin, 5)
     gemm_ms, _ = clock(gemm_only, 5)
     ref_ms, lp_ref = clock(reference, 2)
+    # forward + backward (gradients of hidden and lm_head), as training uses it
+    gout = torch.randn(N, device=dev, generator=g)
+
+    def train(fn):
+        def step():
+            h.grad = None
+            w.grad = None
+            (fn() * gout).sum().backward()
+        return step
+
+    h.requires_grad_(True)
+    w.requires_grad_(True)
+    ours_fb_ms, _ = clock(train(dropin), 2)
+    gh_ours, gw_ours = h.grad.clone(), w.grad.clone()
+    ref_fb_ms, _ = clock(train(reference), 1)
+    grad_diff = max(float((gh_ours - h.grad).abs().max()), float((gw_ours - w.grad).abs().max()))
+    h.requires_grad_(False)
+    w.requires_grad_(False)
+    del gh_ours, gw_ours
+    h.grad = None
+    w.grad = None
     flops = 2.0 * N * H * V
     return {
         "shape": {"tokens": N, "hidden": H, "vocab": V, "chunk": chunk},
@@ -254,8 +275,11 @@ def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
         "gemm_frac_bf16_peak": round(flops / (gemm_ms * 1e-3) / 2.5e15, 4),
         "dropin_tflops": round(flops / (ours_ms * 1e-3) / 1e12, 1),
         "max_abs_diff_vs_reference": round(float((lp - lp_ref).abs().max()), 7),
+        "dropin_fwd_bwd_ms": round(ours_fb_ms, 3), "reference_fwd_bwd_ms": round(ref_fb_ms, 3),
+        "max_abs_grad_diff_vs_reference": round(grad_diff, 9),
         "what": "fp32 inputs holding bf16 values, as the callers pass them; HIP events, "
-                "5 (drop-in, GEMM) and 2 (reference) calls after one warm-up",
+                "5 (drop-in, GEMM) and 2 (reference) forward calls, 2 and 1 forward+backward "
+                "calls, each after one warm-up",
     }
 
 

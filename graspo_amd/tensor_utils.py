@@ -151,19 +151,37 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         mc = saved[4:6] if ctx.has_mc else None
         g = grad_out.reshape(-1).to(torch.float32)
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        grad_h = torch.zeros_like(h2) if need_h else None
+        # the bf16 route accumulates grad_h over the chunks in fp32
+        acc_dtype = torch.float32 if mc is not None else h2.dtype
+        grad_h = torch.zeros(h2.shape, dtype=acc_dtype, device=h2.device) if need_h else None
         grad_w = torch.empty_like(weight) if need_w else None
         for start in range(0, weight.shape[0], ctx.chunk):
             w_c = weight[start : start + ctx.chunk]
             # g * (onehot - softmax) of this chunk's logits, one kernel pass
             logits = _chunk_logits(h2, weight, mc, start, ctx.chunk)
             gc = ops.logprob_backward(logits, t, g, lse, col_offset=start)
+            if mc is not None:
+                # bf16 matrix cores with fp32 output: gc = hi + lo in bf16
+                # (the rest is below 2^-17 |gc|) against the exact bf16
+                # operands, so the products keep fp32-level accuracy
+                hb, wb = mc
+                hi = gc.to(torch.bfloat16)
+                lo = (gc - hi.float()).to(torch.bfloat16)
+                w_b = wb[start : start + ctx.chunk]
+                if need_h:
+                    grad_h += torch.mm(hi, w_b, out_dtype=torch.float32)
+                    grad_h += torch.mm(lo, w_b, out_dtype=torch.float32)
+                if need_w:
+                    gw = (torch.mm(hi.t(), hb, out_dtype=torch.float32)
+                          + torch.mm(lo.t(), hb, out_dtype=torch.float32))
+                    grad_w[start : start + ctx.chunk] = gw.to(weight.dtype)
+                continue
             if need_h:
                 grad_h += gc.to(h2.dtype) @ w_c.to(h2.dtype)
             if need_w:
                 grad_w[start : start + ctx.chunk] = (gc.t() @ h2.to(gc.dtype)).to(weight.dtype)
         if grad_h is not None:
-            grad_h = grad_h.view(*ctx.out_shape, h2.shape[-1])
+            grad_h = grad_h.to(h2.dtype).view(*ctx.out_shape, h2.shape[-1])
         return grad_h, grad_w, None, None
 
 
@@ -179,8 +197,10 @@ def _selected_token_log_probs_from_hidden(
     reference's ``vocab_chunk_size`` GEMMs -- on bf16 matrix cores with fp32
     logits when the operands are bf16 values, as the reference's ``.float()``
     copies are -- and the logsumexp / logaddexp fold is the lse kernel.
-    Differentiable in ``hidden_states`` and ``lm_head_weight`` (the gradient
-    GEMMs stay in the operands' dtype)."""
+    Differentiable in ``hidden_states`` and ``lm_head_weight``; on the bf16
+    route the gradient GEMMs also run on matrix cores, with the fp32 softmax
+    gradient split into two bf16 parts (hi + lo), so the gradients keep
+    fp32-level accuracy."""
     return _SelectedLogProbsFromHidden.apply(
         hidden_states, lm_head_weight, output_ids, int(vocab_chunk_size)
     )
