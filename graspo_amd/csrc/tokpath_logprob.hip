@@ -180,6 +180,42 @@ struct GradOut<float> {
   __device__ static __forceinline__ void put(float* p, int64_t i, float g) { p[i] = g; }
 };
 
+// One row of g * ([i == t] - p_i), p_i = 2^((x_i - lse) log2 e): whole
+// vectors go to emit_vec(vector index, gradients), the elements past the last
+// whole vector (or every element when nvec == 0) to emit_one(i, gradient).
+template <typename T, typename EmitVec, typename EmitOne>
+__device__ __forceinline__ void logprob_backward_row(const T* __restrict__ row, int64_t V,
+                                                     int64_t nvec, int64_t tgt, float g, float lse,
+                                                     EmitVec&& emit_vec, EmitOne&& emit_one) {
+  constexpr int E = Vec<T>::kE;
+  const float ng = -g;
+  stream_vectors<T, kLpBlock, kLpVecs, true>(
+      row, 0, nvec, [&](float(&x)[kLpVecs][E], int64_t vbase, bool last) {
+#pragma unroll
+        for (int k = 0; k < kLpVecs; ++k) {
+          const int64_t vi = vbase + (int64_t)k * kLpBlock;
+          if (last && vi >= nvec) continue;
+          float gr[E];
+#pragma unroll
+          for (int j = 0; j < E; ++j)
+            gr[j] = ng * __builtin_amdgcn_exp2f((x[k][j] - lse) * kLog2e);
+          const int64_t d = tgt - vi * E;
+          if (d >= 0 && d < E) {
+            // g (1 - p_t) as -g expm1(x_t - lse): no cancellation when p_t ~ 1
+#pragma unroll
+            for (int j = 0; j < E; ++j)
+              if (j == (int)d) gr[j] = -g * expm1f(x[k][j] - lse);
+          }
+          emit_vec(vi, gr);
+        }
+      });
+  for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) {
+    const float xi = Elem<T>::get(row, i);
+    emit_one(i, i == tgt ? -g * expm1f(xi - lse)
+                         : ng * __builtin_amdgcn_exp2f((xi - lse) * kLog2e));
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
     const T* __restrict__ logits, int64_t V, int64_t row_stride, int64_t col_offset,
@@ -200,35 +236,66 @@ __global__ __launch_bounds__(kLpBlock) void logprob_backward_kernel(
     for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) GradOut<T>::put(grow, i, 0.0f);
     return;
   }
-  // p_i = 2^((x_i - lse) log2 e); the one-hot term is added where i == t
-  const float lse = lse_in[n];
-  const float ng = -g;
-  stream_vectors<T, kLpBlock, kLpVecs, true>(
-      row, 0, nvec, [&](float(&x)[kLpVecs][E], int64_t vbase, bool last) {
-#pragma unroll
-        for (int k = 0; k < kLpVecs; ++k) {
-          const int64_t vi = vbase + (int64_t)k * kLpBlock;
-          if (last && vi >= nvec) continue;
-          float gr[E];
-#pragma unroll
-          for (int j = 0; j < E; ++j)
-            gr[j] = ng * __builtin_amdgcn_exp2f((x[k][j] - lse) * kLog2e);
-          const int64_t d = tgt - vi * E;
-          if (d >= 0 && d < E) {
-            // g (1 - p_t) as -g expm1(x_t - lse): no cancellation when p_t ~ 1
-#pragma unroll
-            for (int j = 0; j < E; ++j)
-              if (j == (int)d) gr[j] = -g * expm1f(x[k][j] - lse);
-          }
-          __builtin_nontemporal_store(GradOut<T>::pack(gr), gv + vi);
-        }
-      });
-  for (int64_t i = nvec * E + threadIdx.x; i < V; i += kLpBlock) {
-    const float xi = Elem<T>::get(row, i);
-    const float gi = i == tgt ? -g * expm1f(xi - lse)
-                              : ng * __builtin_amdgcn_exp2f((xi - lse) * kLog2e);
-    GradOut<T>::put(grow, i, gi);
+  logprob_backward_row<T>(
+      row, V, nvec, tgt, g, lse_in[n],
+      [&](int64_t vi, const float(&gr)[E]) {
+        __builtin_nontemporal_store(GradOut<T>::pack(gr), gv + vi);
+      },
+      [&](int64_t i, float gi) { GradOut<T>::put(grow, i, gi); });
+}
+
+// The same gradient of fp32 logits written as two bf16 arrays, hi = the
+// gradient rounded to bf16 and lo = the remainder rounded to bf16, so that
+// |grad - hi - lo| <= 2^-16 |grad| (each bf16 rounding is within 2^-8): bf16
+// matrix-core GEMMs of both parts carry about 16 significant bits.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16(float v, uint32_t& hi, uint32_t& lo) {
+  hi = bf16_rne(v);
+  lo = (hi & 0x7F80u) == 0x7F80u ? 0u : bf16_rne(v - u2f(hi << 16));  // inf / NaN: no remainder
+}
+__global__ __launch_bounds__(kLpBlock) void logprob_backward_split_kernel(
+    const float* __restrict__ logits, int64_t V, int64_t row_stride, int64_t col_offset,
+    const void* __restrict__ targets, int t64, const float* __restrict__ grad_lp,
+    const float* __restrict__ lse_in, uint16_t* __restrict__ ghi, uint16_t* __restrict__ glo,
+    int64_t grad_stride) {
+  const int64_t n = blockIdx.x;
+  const float* row = logits + n * row_stride;
+  uint16_t* hrow = ghi + n * grad_stride;
+  uint16_t* lrow = glo + n * grad_stride;
+  const float g = grad_lp[n];
+  const int64_t tgt = load_target(targets, t64, n) - col_offset;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) |
+                       ((reinterpret_cast<uintptr_t>(hrow) | reinterpret_cast<uintptr_t>(lrow)) &
+                        7u)) == 0;
+  const int64_t nvec = vec_ok ? V / 4 : 0;
+  u32x2* hv = reinterpret_cast<u32x2*>(hrow);
+  u32x2* lv = reinterpret_cast<u32x2*>(lrow);
+  if (g == 0.0f) {
+    const u32x2 z = {0u, 0u};
+    for (int64_t vi = threadIdx.x; vi < nvec; vi += kLpBlock) {
+      __builtin_nontemporal_store(z, hv + vi);
+      __builtin_nontemporal_store(z, lv + vi);
+    }
+    for (int64_t i = nvec * 4 + threadIdx.x; i < V; i += kLpBlock) hrow[i] = lrow[i] = 0;
+    return;
   }
+  logprob_backward_row<float>(
+      row, V, nvec, tgt, g, lse_in[n],
+      [&](int64_t vi, const float(&gr)[4]) {
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split_bf16(gr[j], h[j], l[j]);
+        const u32x2 ho = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        const u32x2 lo = {l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+        __builtin_nontemporal_store(ho, hv + vi);
+        __builtin_nontemporal_store(lo, lv + vi);
+      },
+      [&](int64_t i, float gi) {
+        uint32_t h, l;
+        split_bf16(gi, h, l);
+        hrow[i] = (uint16_t)h;
+        lrow[i] = (uint16_t)l;
+      });
 }
 
 }  // namespace gtp
@@ -310,6 +377,24 @@ extern "C" int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_l
 }
 
 extern "C" const char* gtp_version(void) { return "graspo_tokpath 0.2 gfx950"; }
+
+extern "C" int gtp_logprob_backward_split_rows(const float* logits, int64_t N, int64_t V,
+                                               int64_t row_stride, int64_t col_offset,
+                                               const void* targets, int targets_int64,
+                                               const float* grad_logprob, const float* lse,
+                                               uint16_t* grad_hi, uint16_t* grad_lo,
+                                               int64_t grad_stride, void* stream) {
+  if (N < 0 || V <= 0 || row_stride < V || grad_stride < V ||
+      (N > 0 && (!logits || !targets || !grad_logprob || !lse || !grad_hi || !grad_lo)))
+    return GTP_ERR_INVALID_ARGUMENT;
+  if (N > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
+  if (N == 0) return GTP_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(logprob_backward_split_kernel, dim3((unsigned)N), dim3(kLpBlock), 0, s,
+                     logits, V, row_stride, col_offset, targets, targets_int64, grad_logprob,
+                     lse, grad_hi, grad_lo, grad_stride);
+  return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+}
 
 extern "C" int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N, int64_t V,
                                          int64_t row_stride, int64_t col_offset,

@@ -1,7 +1,7 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
-// lse_finalize, decode_update, to_bf16_exact}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lse_finalize, decode_update, to_bf16_exact, logprob_backward_split}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -375,6 +375,37 @@ void decode_update(const at::Tensor& ids, const c10::optional<at::Tensor>& statu
   check_rc(rc, "gtp_decode_update_rows");
 }
 
+// (hi, lo) bf16 parts of the logprob gradient of fp32 logits [N, V]
+std::tuple<at::Tensor, at::Tensor> logprob_backward_split(const at::Tensor& logits,
+                                                          const at::Tensor& targets,
+                                                          const at::Tensor& grad_logprob,
+                                                          const at::Tensor& lse,
+                                                          int64_t col_offset, int64_t stream) {
+  check_rows(logits, "logits");
+  TORCH_CHECK(logits.scalar_type() == at::kFloat,
+              "graspo_tokpath.logprob_backward_split: logits must be float32");
+  const int64_t N = logits.size(0), V = logits.size(1);
+  check_same_device(logits, targets, "targets");
+  check_same_device(logits, grad_logprob, "grad_logprob");
+  check_same_device(logits, lse, "lse");
+  TORCH_CHECK((targets.scalar_type() == at::kInt || targets.scalar_type() == at::kLong) &&
+                  targets.numel() == N && targets.is_contiguous(),
+              "graspo_tokpath.logprob_backward_split: targets must be int32/int64 [N]");
+  TORCH_CHECK(grad_logprob.scalar_type() == at::kFloat && grad_logprob.numel() == N &&
+                  grad_logprob.is_contiguous() && lse.scalar_type() == at::kFloat &&
+                  lse.numel() == N && lse.is_contiguous(),
+              "graspo_tokpath.logprob_backward_split: grad_logprob and lse must be float32 [N]");
+  at::Tensor hi = at::empty({N, V}, logits.options().dtype(at::kBFloat16));
+  at::Tensor lo = at::empty({N, V}, logits.options().dtype(at::kBFloat16));
+  const int rc = gtp_logprob_backward_split_rows(
+      logits.data_ptr<float>(), N, V, row_stride_of(logits), col_offset, targets.data_ptr(),
+      targets.scalar_type() == at::kLong ? 1 : 0, grad_logprob.data_ptr<float>(),
+      lse.data_ptr<float>(), static_cast<uint16_t*>(hi.data_ptr()),
+      static_cast<uint16_t*>(lo.data_ptr()), V, reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_logprob_backward_split_rows");
+  return {hi, lo};
+}
+
 // bf16 copy of a contiguous fp32 tensor, and whether any value was not a bf16
 // value (a device flag the caller reads)
 std::tuple<at::Tensor, at::Tensor> to_bf16_exact(const at::Tensor& src, int64_t stream) {
@@ -425,4 +456,8 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "Tensor(d!) flags, int stream) -> ()",
       &decode_update);
   m.def("to_bf16_exact(Tensor src, int stream) -> (Tensor, Tensor)", &to_bf16_exact);
+  m.def(
+      "logprob_backward_split(Tensor logits, Tensor targets, Tensor grad_logprob, Tensor lse, "
+      "int col_offset, int stream) -> (Tensor, Tensor)",
+      &logprob_backward_split);
 }

@@ -120,6 +120,20 @@ def logprob_backward(logits: torch.Tensor, targets: torch.Tensor, grad_logprob: 
         lse.reshape(-1).to(torch.float32).contiguous(), int(col_offset), out, _stream(logits))
 
 
+def logprob_backward_split(logits: torch.Tensor, targets: torch.Tensor,
+                           grad_logprob: torch.Tensor, lse: torch.Tensor, col_offset: int = 0):
+    """The logprob gradient of fp32 ``logits`` [N, V] as two bf16 [N, V]
+    tensors (hi, lo) with |grad - hi - lo| <= 2^-16 |grad|."""
+    ops = load()
+    logits = _as_rows(logits)
+    targets = targets.reshape(-1)
+    if targets.dtype not in (torch.int32, torch.int64):
+        targets = targets.to(torch.int64)
+    return ops.logprob_backward_split(
+        logits, targets.contiguous(), grad_logprob.reshape(-1).to(torch.float32).contiguous(),
+        lse.reshape(-1).to(torch.float32).contiguous(), int(col_offset), _stream(logits))
+
+
 def graspo_loss_forward(log_probs: torch.Tensor, old_log_probs: torch.Tensor,
                         advantages: torch.Tensor, action_mask: torch.Tensor | None,
                         clip_lo: float, clip_hi: float):

@@ -159,14 +159,14 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
             w_c = weight[start : start + ctx.chunk]
             # g * (onehot - softmax) of this chunk's logits, one kernel pass
             logits = _chunk_logits(h2, weight, mc, start, ctx.chunk)
-            gc = ops.logprob_backward(logits, t, g, lse, col_offset=start)
             if mc is not None:
-                # bf16 matrix cores with fp32 output: gc = hi + lo in bf16
-                # (the rest is below 2^-17 |gc|) against the exact bf16
-                # operands, so the products keep fp32-level accuracy
+                # bf16 matrix cores with fp32 output: the gradient kernel
+                # writes gc = hi + lo in bf16 (|gc - hi - lo| <= 2^-16 |gc|),
+                # multiplied against the exact bf16 operands: the products
+                # carry about 16 significant bits
                 hb, wb = mc
-                hi = gc.to(torch.bfloat16)
-                lo = (gc - hi.float()).to(torch.bfloat16)
+                hi, lo = ops.logprob_backward_split(logits, t, g, lse, col_offset=start)
+                del logits
                 w_b = wb[start : start + ctx.chunk]
                 if need_h:
                     grad_h += torch.mm(hi, w_b, out_dtype=torch.float32)
@@ -176,6 +176,7 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
                           + torch.mm(lo.t(), hb, out_dtype=torch.float32))
                     grad_w[start : start + ctx.chunk] = gw.to(weight.dtype)
                 continue
+            gc = ops.logprob_backward(logits, t, g, lse, col_offset=start)
             if need_h:
                 grad_h += gc.to(h2.dtype) @ w_c.to(h2.dtype)
             if need_w:
@@ -199,8 +200,8 @@ def _selected_token_log_probs_from_hidden(
     copies are -- and the logsumexp / logaddexp fold is the lse kernel.
     Differentiable in ``hidden_states`` and ``lm_head_weight``; on the bf16
     route the gradient GEMMs also run on matrix cores, with the fp32 softmax
-    gradient split into two bf16 parts (hi + lo), so the gradients keep
-    fp32-level accuracy."""
+    gradient split into two bf16 parts (hi + lo, within 2^-16 of it), so the
+    gradients carry about 16 significant bits."""
     return _SelectedLogProbsFromHidden.apply(
         hidden_states, lm_head_weight, output_ids, int(vocab_chunk_size)
     )

@@ -211,6 +211,24 @@ int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N,
                               int64_t grad_stride, void* stream);
 
 /*
+ * gtp_logprob_backward_split_rows -- the gradient of gtp_logprob_backward_rows
+ * for fp32 logits, written as two bf16 arrays: grad_hi = the gradient rounded
+ * to bf16, grad_lo = the remainder rounded to bf16, so that
+ * |grad - hi - lo| <= 2^-16 |grad| (lo = 0 where hi is not finite): about 16
+ * significant bits.  Feeds the hidden-state path's backward
+ * (tensor_utils.py:167-186 under autograd) into bf16 matrix-core GEMMs with
+ * fp32 output.
+ * Arguments as gtp_logprob_backward_rows; grad_hi and grad_lo share
+ * grad_stride.
+ */
+int gtp_logprob_backward_split_rows(const float* logits, int64_t N, int64_t V,
+                                    int64_t row_stride, int64_t col_offset,
+                                    const void* targets, int targets_int64,
+                                    const float* grad_logprob, const float* lse,
+                                    uint16_t* grad_hi, uint16_t* grad_lo,
+                                    int64_t grad_stride, void* stream);
+
+/*
  * gtp_graspo_loss_forward / gtp_graspo_loss_backward -- the GRASPO PPO-clip
  * surrogate over token logprobs, fused:
  *   loss = mean_b( sum_t m l / max(1, sum_t m) ),

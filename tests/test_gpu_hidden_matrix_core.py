@@ -104,3 +104,35 @@ def test_hidden_path_gradients_on_the_bf16_route():
     assert float((out.double() - ref).abs().max()) <= 1e-4
     assert float((h.grad.double() - h2.grad).abs().max()) <= 1e-4
     assert float((w.grad.double() - w2.grad).abs().max()) <= 1e-4
+
+
+@pytest.mark.parametrize("V", [4099, 32768])
+def test_split_gradient_is_the_fp32_gradient(V):
+    """gtp_logprob_backward_split_rows: hi and lo are bf16 with hi the fp32
+    gradient rounded to bf16 and |grad - hi - lo| <= 2^-16 |grad| (each bf16
+    rounding is within 2^-8; + a tiny absolute floor), against the fp32 gradient kernel and fp64; rows with
+    g == 0 are zeros; a column offset moves the one-hot term."""
+    g0 = torch.Generator().manual_seed(V)
+    N = 12
+    x = (torch.randn(N, V, generator=g0) * 3.0).to(DEV)
+    t = torch.randint(0, V, (N,), generator=g0).to(DEV)
+    g = torch.randn(N, generator=g0).to(DEV)
+    g[2] = 0.0
+    x[4, 9] = 50.0
+    t[4] = 9  # one-hot spike: the gradient is ~0 everywhere, computed without cancellation
+    lse = torch.logsumexp(x.double(), dim=1).float()
+    for off in (0, 17):
+        hi, lo = ops.logprob_backward_split(x, t + off, g, lse, col_offset=off)
+        full = ops.logprob_backward(x, t + off, g, lse, col_offset=off)
+        torch.cuda.synchronize()
+        assert torch.equal(hi, full.to(torch.bfloat16))
+        s = hi.float() + lo.float()
+        assert float(((s - full).abs() - full.abs() * 2.0 ** -16 - 1e-30).max()) <= 0.0
+        xd = x.double()
+        p = torch.exp(xd - lse.double().unsqueeze(1))
+        ref = -g.double().unsqueeze(1) * p
+        ref[torch.arange(N), t] += g.double()
+        # the fp32 gradient's own bound (tests/test_gpu_logprob_backward.py)
+        # plus the split's 2^-16
+        assert float(((s.double() - ref).abs() - (2e-6 + 2.0 ** -16) * ref.abs() - 1e-7).max()) <= 0.0
+        assert not bool(hi[2].float().any()) and not bool(lo[2].float().any())
