@@ -478,19 +478,24 @@ __device__ __forceinline__ unsigned long long radix_kth(FastSmem& sm, uint32_t k
   return prefix;
 }
 
-// Rank of each of n <= kFT distinct keys by counting (one broadcast LDS read
-// per wave per key); entries of rank < k go to out(rank, key, x).
-// Block-uniform; callers sync before (keys complete).
+// Rank of each of n <= kFT / 4 distinct keys by counting: the four threads
+// of a quad share a key and each counts the larger keys in a quarter of the
+// list, summed within the quad (DPP); entries of rank < k go to
+// out(rank, key, x).  Block-uniform; callers sync before (keys complete).
 template <typename Out>
 __device__ __forceinline__ void rank_sort_small(const unsigned long long* keys, const float* xs,
                                                 uint32_t n, uint32_t k, Out out) {
-  if (threadIdx.x < n) {
-    const unsigned long long ki = keys[threadIdx.x];
-    uint32_t rk = 0;
-#pragma unroll 8
-    for (uint32_t j = 0; j < n; ++j) rk += keys[j] > ki ? 1u : 0u;
-    if (rk < k) out(rk, ki, xs[threadIdx.x]);
+  const uint32_t i = threadIdx.x >> 2, part = threadIdx.x & 3u;
+  unsigned long long ki = 0;
+  uint32_t rk = 0;
+  if (i < n) {
+    ki = keys[i];
+#pragma unroll 4
+    for (uint32_t j = part; j < n; j += 4u) rk += keys[j] > ki ? 1u : 0u;
   }
+  rk += lane_xor<1>(rk);  // every lane takes part in the quad sums
+  rk += lane_xor<2>(rk);
+  if (i < n && part == 0u && rk < k) out(rk, ki, xs[i]);
 }
 
 // The slice's top Kc into sm.skey / sm.sx (unsorted) when more than 256
@@ -997,9 +1002,24 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
       }
     }
   }
-  bad_hist = __syncthreads_or(bad_hist);  // also completes the pool and the bitmap
-  float lm = st.m, ls = st.s;
-  block_lse2<kFT>(lm, ls, sm.red);
+  // each wave's raw (m, s) goes to LDS with the barrier below; only the
+  // finish (or the slice's head) needs the merged value, so no barrier of its
+  // own sits on the path
+  {
+    float wm = st.m, ws = st.s;
+    wave_lse2(wm, ws);
+    if (lane == 0) {
+      sm.red[wid][0] = wm;
+      sm.red[wid][1] = ws;
+    }
+  }
+  bad_hist = __syncthreads_or(bad_hist);  // also completes the pool, the bitmap and the sums
+  // the merged raw log-sum-exp, for the calling wave (wave 0 uses it)
+  auto merged_lse = [&](float& lm, float& ls) __attribute__((always_inline)) {
+    lm = lane < kFWaves ? sm.red[lane][0] : kNegInf;
+    ls = lane < kFWaves ? sm.red[lane][1] : 0.0f;
+    wave_lse2(lm, ls);
+  };
 
   // ---- 2. resolve the pool: exact processed logits and order keys.  Every
   // token left out has x < theta, so its processed logit is <= yex; the pool
@@ -1252,14 +1272,21 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   }
   __syncthreads();
   if (S == 1) {
+    if (tid >= kWave) return;
+    float lm, ls;
+    merged_lse(lm, ls);
     finish_row(sm, fa, b, u_row, lm, ls, bad_hist, nout);
     return;
   }
-  if (tid == 0) {
-    head->m = lm;
-    head->s = ls;
-    head->n = nout;
-    head->flags = (s == 0 && bad_hist) ? 1u : 0u;
+  if (tid < kWave) {
+    float lm, ls;
+    merged_lse(lm, ls);
+    if (tid == 0) {
+      head->m = lm;
+      head->s = ls;
+      head->n = nout;
+      head->flags = (s == 0 && bad_hist) ? 1u : 0u;
+    }
   }
 
   // ---- 4. the last workgroup of the row to arrive merges.  The barrier
