@@ -17,6 +17,20 @@ from torch.nn import functional as F  # noqa: N812
 from . import ops
 
 
+def _bf16_when_exact(logits: torch.Tensor, temperature: float, top_k: int) -> torch.Tensor:
+    """fp32 rows as their bf16 copy when every value is a bf16 value -- the
+    reference's callers pass ``logits.float()`` of a bf16 model -- and the
+    call would otherwise take the row-wise kernel (sampling without a top-k
+    of at most 128): the value-histogram kernel takes bf16 rows only, and the
+    samples are the same because the float inputs are.  Costs one pass over
+    the rows and one host synchronisation."""
+    if (logits.dtype != torch.float32 or logits.dim() != 2 or not logits.is_cuda
+            or not temperature > 0 or 1 <= top_k <= 128):
+        return logits
+    bf, inexact = ops.to_bf16_exact(logits)
+    return bf if int(inexact) == 0 else logits
+
+
 def _next_token_from_logits(
     logits: torch.Tensor,
     *,
@@ -35,7 +49,11 @@ def _next_token_from_logits(
     ``temperature <= 0`` is greedy (argmax, lowest id on ties); otherwise the
     row is divided by ``max(temperature, 1e-6)`` and sampled under top-k /
     top-p from ``uniforms`` (drawn from torch's generator when omitted, as the
-    reference's ``torch.multinomial`` does).  Returns int64 [B]."""
+    reference's ``torch.multinomial`` does).  Returns int64 [B].  fp32 rows
+    holding bf16 values take the bf16 kernels when the status is checked
+    (that check synchronises anyway)."""
+    if check_status:
+        logits = _bf16_when_exact(logits, float(temperature), int(top_k))
     out = ops.sample(
         logits,
         temperature=float(temperature),

@@ -136,3 +136,29 @@ def test_split_gradient_is_the_fp32_gradient(V):
         # plus the split's 2^-16
         assert float(((s.double() - ref).abs() - (2e-6 + 2.0 ** -16) * ref.abs() - 1e-7).max()) <= 0.0
         assert not bool(hi[2].float().any()) and not bool(lo[2].float().any())
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_fp32_top_p_rows_take_the_bf16_kernel_when_exact(exact):
+    """_next_token_from_logits on fp32 rows holding bf16 values (as the
+    reference's logits.float() are) samples them through the bf16 kernels and
+    returns exactly the ids of the bf16 rows and of the oracle on the fp32
+    values; rows that are not bf16 values keep the fp32 path and still match
+    the oracle."""
+    from tests._util import oracle_sample
+
+    g = torch.Generator().manual_seed(21)
+    B, V = 16, 151936
+    xb = (torch.randn(B, V, generator=g) * 2.5).to(torch.bfloat16)
+    x32 = xb.float()
+    if not exact:
+        x32 = x32 + 1e-4 * torch.randn(B, V, generator=g)
+    u = (torch.randint(0, 1 << 24, (B,), generator=g).float() * 2.0 ** -24)
+    kw = dict(temperature=0.8, top_p=0.9, uniforms=u.to(DEV))
+    print("fp32 top-p route", exact, flush=True)
+    ids32 = TU._next_token_from_logits(x32.to(DEV), **kw)
+    want = oracle_sample(x32, temperature=0.8, top_p=0.9, uniforms=u)
+    assert torch.equal(ids32.cpu(), torch.from_numpy(want.ids)), exact
+    if exact:
+        idsb = TU._next_token_from_logits(xb.to(DEV), **kw)
+        assert torch.equal(ids32, idsb)
