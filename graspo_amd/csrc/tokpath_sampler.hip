@@ -910,8 +910,9 @@ __global__ __launch_bounds__(kSB) void sampler_rowwise_kernel(SamplerArgs a) {
 //    singletons, sorted in registers) merged by position, and a penalised
 //    value equal to a bin's y merged into that bin.  A run of tokens with
 //    one value has one weight, so positions inside it are integer quotients.
-// 4. A token of a bin is found by id: one rescan of the row counts the
-//    bin's tokens per thread range, in id order.
+// 4. A token of a bin is found by id: one coalesced rescan of the row lists
+//    each wave's members of the two items in id order (a packed 16-bit
+//    compare of 8 tokens against a pattern costs 13 instructions).
 // Anything outside these bounds -- more singletons than the list holds, a
 // singleton or penalised value exactly tied with another item at a cut,
 // more than 64 extra items in one resolved segment, a non-finite processed
@@ -930,6 +931,20 @@ constexpr int kHItems = kHSegBins + kHXCap;
 constexpr int kHPenSpan = 2048;          // penalised-value bins one segment may span
 constexpr int kHG = 2;                   // vectors per thread per stream step
 constexpr uint32_t kNoPattern = 0x10000u;  // matches no 16-bit pattern
+constexpr int kHListCap = 512;
+
+// Set lanes of a wave mask below this lane.
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Lane-wise minimum of the two unsigned 16-bit halves (v_pk_min_u16; the
+// compiler turns the generic form into compares and selects).
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}           // ids of one item one wave lists in the rescan
 
 struct alignas(16) HistSmem {
   uint32_t cnt[kHBins + kWave];          // allowed unpenalised tokens per value (+ a spill word per lane)
@@ -966,8 +981,11 @@ struct alignas(16) HistSmem {
   uint32_t res_c, res_cb;
   unsigned long long res_wb, res_w;
   int32_t id_out[2];
+  int32_t walk_w[2];
+  uint32_t walk_lo[2];
 };
 static_assert(sizeof(HistSmem) <= 160 * 1024, "one workgroup per CU");
+static_assert(2 * kSW * kHListCap <= kHBins + kWave, "the id lists fit in the bin counts");
 
 // Block maximum of a float (every thread gets it).
 __device__ __forceinline__ float block_max_hist(HistSmem& sm, float v) {
@@ -1620,7 +1638,6 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   unsigned long long W_K = W_all, Wp = 0, w_draw = 0;
   uint32_t R = nk;
   int32_t thr_ref = 0, thr_aux = -1, thr_j = 0, drw_ref = 0, drw_aux = -1, drw_j = 0;
-  uint32_t thr_c = 0, drw_c = 0;
   bool have_thr = false;
   for (int step = 0; step < 4; ++step) {
     if ((step == 0 && !k_active) || (step == 1 && !p_active) || (step == 2 && have_thr)) continue;
@@ -1643,7 +1660,6 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       thr_ref = sm.res_ref;
       thr_aux = sm.res_aux;
       thr_j = sm.res_j;
-      thr_c = sm.res_c;
       Wp = S_after;
       have_thr = step != 0 || !p_active;
     } else if (step == 1) {
@@ -1652,7 +1668,6 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
       drw_ref = sm.res_ref;
       drw_aux = sm.res_aux;
       drw_j = sm.res_j;
-      drw_c = sm.res_c;
       w_draw = sm.res_w;
     }
   }
@@ -1660,9 +1675,13 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
   // ---- 4. ids: a singleton's is known; otherwise the j-th token, in id
   // order, among the allowed tokens with the item's bit pattern (unpenalised
   // for a bin, penalised for a penalised value; both for a merged bin).
-  // Thread t scans a contiguous range of vectors; a one-token item takes the
-  // first match, else per-thread counts pick the thread whose range the
-  // walker's wave reads again, one vector a lane.
+  // Wave w rescans the w-th sixteenth of the row, 64 consecutive vectors a
+  // step, one a lane; a step with no token equal to a pattern costs only the
+  // compares.  The members found in a step are appended to the wave's list
+  // of each item in id order (a prefix over the lanes), so the j-th member
+  // is read from the list of the wave whose count covers j.  A list holds
+  // kHListCap ids (in the bin counts' storage, read no more); a member past
+  // that is found by scanning the wave's range again for that position only.
   uint32_t hu1 = kNoPattern, hp1 = kNoPattern, hu2 = kNoPattern, hp2 = kNoPattern;
   if (thr_ref >= kHBins) {
     hp1 = hbin_bits(thr_ref - kHBins);
@@ -1677,135 +1696,183 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
     if (drw_aux >= 0) hp2 = hbin_bits(drw_aux);
   }
   const bool need1 = thr_ref >= 0, need2 = drw_ref >= 0;
-  const bool one1 = need1 && thr_c == 1u, one2 = need2 && drw_c == 1u;
-  const bool any_pp = hp1 != kNoPattern || hp2 != kNoPattern;  // a penalised pattern to match
   __syncthreads();
   if (tid == 0) {
     sm.id_out[0] = need1 ? -1 : (int32_t)sm.sid[-1 - thr_ref];
     sm.id_out[1] = need2 ? -1 : (int32_t)sm.sid[-1 - drw_ref];
+    sm.walk_w[0] = sm.walk_w[1] = -1;
   }
   if (need1 || need2) {
     const int64_t nv8 = (V + 7) / 8;
-    const int64_t span = (nv8 + kSB - 1) / kSB;
-    const int64_t t0 = (int64_t)tid * span < nv8 ? (int64_t)tid * span : nv8;
-    const int64_t t1 = t0 + span < nv8 ? t0 + span : nv8;
-    // members of the two items among the 8 tokens (bit patterns hv) from e0:
-    // low byte item 1, high byte item 2
-    auto members = [&](const uint32_t (&hv)[8], int64_t e0) __attribute__((always_inline)) -> uint32_t {
-      uint32_t ok = 0xFFu;
-      if (kMask) ok = (mrow[e0 >> 5] >> (e0 & 31)) & 0xFFu;
-      uint32_t m1 = 0, m2 = 0;
-      if (any_pp) {
-        const uint32_t pn = use_pen ? (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu : 0u;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const bool pj = (pn >> j) & 1u;
-          m1 |= (hv[j] == (pj ? hp1 : hu1) ? 1u : 0u) << j;
-          m2 |= (hv[j] == (pj ? hp2 : hu2) ? 1u : 0u) << j;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          m1 |= (hv[j] == hu1 ? 1u : 0u) << j;
-          m2 |= (hv[j] == hu2 ? 1u : 0u) << j;
-        }
-        if (use_pen) {
-          const uint32_t pn = (sm.pen[e0 >> 5] >> (e0 & 31)) & 0xFFu;
-          if ((m1 | m2) & pn) {
-            m1 &= ~pn;
-            m2 &= ~pn;
-          }
-        }
-      }
-      return (m1 & ok) | ((m2 & ok) << 8);
+    const int64_t wspan = ((nv8 + kSW - 1) / kSW + 7) & ~(int64_t)7;  // whole 128-byte lines
+    // Bit j set: token j of the vector w (tokens 2k and 2k+1 in the low and
+    // high half of word k) differs from the pattern pp (the 16-bit pattern in
+    // both halves).  Per word a packed 16-bit min(w ^ pp, 1) is 0 in a
+    // matching half and 1 otherwise; the halves' bits are then interleaved.
+    auto nomatch = [](const u32x4& w, uint32_t pp) __attribute__((always_inline)) -> uint32_t {
+      const uint32_t z0 = pk_min_u16(w.x ^ pp, 0x00010001u), z1 = pk_min_u16(w.y ^ pp, 0x00010001u);
+      const uint32_t z2 = pk_min_u16(w.z ^ pp, 0x00010001u), z3 = pk_min_u16(w.w ^ pp, 0x00010001u);
+      const uint32_t q = z0 | (z1 << 2) | (z2 << 4) | (z3 << 6);  // even tokens at 0-6, odd at 16-22
+      return (q & 0xFFFFu) | (q >> 15);
     };
-    auto members_at = [&](int64_t vi) __attribute__((always_inline)) -> uint32_t {
+    // the patterns are the same in every lane: keep them in scalar registers
+    const uint32_t pu1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(hu1 * 0x10001u));
+    const uint32_t pp1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(hp1 * 0x10001u));
+    const uint32_t pu2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(hu2 * 0x10001u));
+    const uint32_t pp2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(hp2 * 0x10001u));
+    const uint32_t hp1s = (uint32_t)__builtin_amdgcn_readfirstlane((int)hp1);
+    const uint32_t hp2s = (uint32_t)__builtin_amdgcn_readfirstlane((int)hp2);
+    // kNoPattern * 0x10001 = 0x10000 (no 16-bit pattern): the item has no such tokens
+    const int en_u1 = __builtin_amdgcn_readfirstlane((int)(pu1 != 0x10000u));
+    const int en_u2 = __builtin_amdgcn_readfirstlane((int)(pu2 != 0x10000u));
+    const int en_p = __builtin_amdgcn_readfirstlane((int)(pp1 != 0x10000u || pp2 != 0x10000u));
+    // Members of the two items among the 8 tokens of vector vi (w; valid:
+    // the tokens inside the row): low byte item 1, high byte item 2.  A
+    // penalised token is a member when it has the item's penalised pattern
+    // (few tokens are penalised: each is compared by itself), any other when
+    // it has the unpenalised one; kNoPattern matches nothing.
+    auto members = [&](const u32x4& w, int64_t vi, uint32_t valid, uint32_t okw, uint32_t pnw)
+        __attribute__((always_inline)) -> uint32_t {
       const int64_t e0 = vi * 8;
-      uint32_t hv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) hv[j] = e0 + j < V ? (uint32_t)row[e0 + j] : 0x10001u;
-      return members(hv, e0);
-    };
-    auto words = [](const u32x4& r, uint32_t (&hv)[8]) __attribute__((always_inline)) {
-      const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) hv[j] = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
-    };
-    const int64_t vlast = t1 < nvec ? t1 : nvec;  // full vectors of the range end here
-    uint32_t c1 = 0, c2 = 0;
-#pragma unroll 1
-    for (int64_t s = t0; s < vlast; s += 8) {
-      u32x4 buf[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int64_t vi = s + i < vlast ? s + i : vlast - 1;
-        buf[i] = *reinterpret_cast<const u32x4*>(row + vi * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (s + i < vlast) {
-          uint32_t hv[8];
-          words(buf[i], hv);
-          const uint32_t mm = members(hv, (s + i) * 8);
-          c1 += (uint32_t)__builtin_popcount(mm & 0xFFu);
-          c2 += (uint32_t)__builtin_popcount(mm >> 8);
-          if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)((s + i) * 8 + __builtin_ctz(mm & 0xFFu));
-          if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)((s + i) * 8 + __builtin_ctz(mm >> 8));
+      uint32_t ok = valid;
+      if (kMask) ok &= okw >> (e0 & 31);
+      const uint32_t pn = use_pen ? (pnw >> (e0 & 31)) & 0xFFu : 0u;
+      const uint32_t nu1 = en_u1 ? nomatch(w, pu1) : 0xFFu;
+      const uint32_t nu2 = en_u2 ? nomatch(w, pu2) : 0xFFu;
+      uint32_t mp = 0;  // penalised members: item 1 in the low byte, item 2 in the high byte
+      if (en_p) {
+        for (uint32_t m = pn & ok; m; m &= m - 1u) {
+          const uint32_t j = (uint32_t)__builtin_ctz(m);
+          const uint32_t wk = j < 4u ? (j < 2u ? w.x : w.y) : (j < 6u ? w.z : w.w);
+          const uint32_t h = (wk >> ((j & 1u) * 16u)) & 0xFFFFu;
+          mp |= ((h == hp1s ? 1u : 0u) | (h == hp2s ? 0x100u : 0u)) << j;
         }
       }
-    }
-    if (t0 <= nvec && nvec < t1) {  // the partial last vector
-      const uint32_t mm = members_at(nvec);
-      c1 += (uint32_t)__builtin_popcount(mm & 0xFFu);
-      c2 += (uint32_t)__builtin_popcount(mm >> 8);
-      if (one1 && (mm & 0xFFu)) sm.id_out[0] = (int32_t)(nvec * 8 + __builtin_ctz(mm & 0xFFu));
-      if (one2 && (mm >> 8)) sm.id_out[1] = (int32_t)(nvec * 8 + __builtin_ctz(mm >> 8));
-    }
-    // exclusive prefix of the counts in thread order
-    const uint32_t i1 = wave_scan_u32(c1), i2 = wave_scan_u32(c2);
-    __syncthreads();
-    if (lane == 0) {
-      sm.red_u[wid] = lane63_u32(i1);
-      sm.red_v[wid] = lane63_u32(i2);
-    }
-    __syncthreads();
-    uint32_t p1 = i1 - c1, p2 = i2 - c2;
+      const uint32_t keep = ~pn & ok;
+      return ((~nu1 & keep) | ((~nu2 & keep) << 8) | mp) & 0xFFFFu;
+    };
+    // This wave's pass over the vectors [r0, r1): member p (from 0, in id
+    // order) of item k goes to dst_k[p - lo_k] when p - lo_k < cap_k; n_k
+    // returns the item's members in the range.
+    auto collect = [&](int64_t r0, int64_t r1, int32_t* dst1, uint32_t lo1, uint32_t cap1,
+                       int32_t* dst2, uint32_t lo2, uint32_t cap2, uint32_t& n1, uint32_t& n2)
+        __attribute__((always_inline)) {
+      constexpr int kU = 8;
+      const int64_t vend = r1 < nvec ? r1 : nvec;  // full vectors of the range end here
+      n1 = 0;
+      n2 = 0;
+#pragma unroll 1
+      for (int64_t s = r0; s < r1; s += (int64_t)kWave * kU) {
+        u32x4 buf[kU];
+        uint32_t okw[kU], pnw[kU];
+        if (vend > r0) {
 #pragma unroll
-    for (int w = 0; w < kSW; ++w)
-      if (w < wid) {
-        p1 += sm.red_u[w];
-        p2 += sm.red_v[w];
-      }
-    const bool walk1 = need1 && !one1 && (uint32_t)thr_j >= p1 && (uint32_t)thr_j < p1 + c1;
-    const bool walk2 = need2 && !one2 && (uint32_t)drw_j >= p2 && (uint32_t)drw_j < p2 + c2;
-    // the wave holding a walker reads the walker's range, one vector a lane
-    // (a range is at most 64 vectors)
+          for (int i = 0; i < kU; ++i) {
+            const int64_t vi = s + i * kWave + lane, vc = vi < vend ? vi : vend - 1;
+            buf[i] = *reinterpret_cast<const u32x4*>(row + vc * 8);
+            if (kMask) okw[i] = mrow[vc >> 2];
+          }
+          if (use_pen) {
 #pragma unroll
-    for (int which = 0; which < 2; ++which) {
-      const unsigned long long wk = __ballot(which == 0 ? walk1 : walk2);
-      if (wk) {
-        const int src = __builtin_ctzll(wk);
-        const int64_t r0 = (int64_t)__builtin_amdgcn_readlane((int)t0, src);
-        const int64_t r1 = (int64_t)__builtin_amdgcn_readlane((int)t1, src);
-        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(which == 0 ? p1 : p2), src);
-        const uint32_t jt = (uint32_t)(which == 0 ? thr_j : drw_j);
-        const int64_t vi = r0 + lane;
-        uint32_t mm = 0;
-        if (vi < r1) {
-          if (vi < nvec) {
-            uint32_t hv[8];
-            words(*reinterpret_cast<const u32x4*>(row + vi * 8), hv);
-            mm = members(hv, vi * 8);
-          } else {
-            mm = members_at(vi);
+            for (int i = 0; i < kU; ++i) {
+              const int64_t vi = s + i * kWave + lane;
+              pnw[i] = sm.pen[(vi < vend ? vi : vend - 1) >> 2];
+            }
           }
         }
-        const uint32_t mine = which == 0 ? (mm & 0xFFu) : (mm >> 8);
-        const uint32_t n = (uint32_t)__builtin_popcount(mine);
-        const uint32_t ex = base + wave_scan_u32(n) - n;
-        if (n && jt >= ex && jt < ex + n)
-          sm.id_out[which] = (int32_t)(vi * 8 + nth_bit(mine, jt - ex));
+#pragma unroll
+        for (int i = 0; i < kU; ++i) {
+          const int64_t vi = s + i * kWave + lane;
+          u32x4 w = buf[i];
+          uint32_t valid = 0xFFu, okv = kMask ? okw[i] : 0u, pnv = use_pen ? pnw[i] : 0u;
+          if (vi >= vend) {
+            // the partial last vector, or past the range
+            valid = 0u;
+            w = u32x4{0u, 0u, 0u, 0u};
+            if (vi < r1) {
+              const int64_t e0 = vi * 8;
+              uint32_t hv[8];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) hv[j] = e0 + j < V ? (uint32_t)row[e0 + j] : 0u;
+              w = u32x4{hv[0] | hv[1] << 16, hv[2] | hv[3] << 16, hv[4] | hv[5] << 16, hv[6] | hv[7] << 16};
+              valid = (1u << (uint32_t)(V - e0)) - 1u;
+              if (kMask) okv = mrow[e0 >> 5];
+              if (use_pen) pnv = sm.pen[e0 >> 5];
+            }
+          }
+          const uint32_t mm = members(w, vi < r1 ? vi : r1 - 1, valid, okv, pnv);  // past the range: none
+          if (__ballot(mm != 0u)) {
+            const uint32_t m1 = mm & 0xFFu, m2 = mm >> 8;
+            const uint32_t c = (uint32_t)__builtin_popcount(m1) | ((uint32_t)__builtin_popcount(m2) << 16);
+            uint32_t ex, tot;
+            if (__ballot((c & 0xFFFEFFFEu) != 0u)) {
+              // a lane with two members of an item: both counts in one scan (a
+              // step holds at most 512 members of an item)
+              const uint32_t inc = wave_scan_u32(c);
+              tot = lane63_u32(inc);
+              ex = inc - c;
+            } else {
+              // at most one member of each item a lane: the lanes below with one
+              const unsigned long long b1 = __ballot(m1 != 0u), b2 = __ballot(m2 != 0u);
+              ex = lanes_below(b1) | (lanes_below(b2) << 16);
+              tot = (uint32_t)__builtin_popcountll(b1) | ((uint32_t)__builtin_popcountll(b2) << 16);
+            }
+            // p - lo in unsigned arithmetic: positions before lo wrap past cap
+            uint32_t q1 = n1 + (ex & 0xFFFFu) - lo1, q2 = n2 + (ex >> 16) - lo2;
+            for (uint32_t m = m1; m; m &= m - 1u, ++q1)
+              if (q1 < cap1) dst1[q1] = (int32_t)(vi * 8 + __builtin_ctz(m));
+            for (uint32_t m = m2; m; m &= m - 1u, ++q2)
+              if (q2 < cap2) dst2[q2] = (int32_t)(vi * 8 + __builtin_ctz(m));
+            n1 += tot & 0xFFFFu;
+            n2 += tot >> 16;
+          }
+        }
       }
+    };
+    int32_t* const lists = reinterpret_cast<int32_t*>(sm.cnt);
+    auto wave_range = [&](int w, int64_t& r0, int64_t& r1) __attribute__((always_inline)) {
+      r0 = (int64_t)w * wspan < nv8 ? (int64_t)w * wspan : nv8;
+      r1 = r0 + wspan < nv8 ? r0 + wspan : nv8;
+    };
+    {
+      int64_t r0, r1;
+      wave_range(wid, r0, r1);
+      int32_t* const l1 = lists + (size_t)wid * 2 * kHListCap;
+      uint32_t n1, n2;
+      collect(r0, r1, l1, 0u, need1 ? (uint32_t)kHListCap : 0u, l1 + kHListCap, 0u,
+              need2 ? (uint32_t)kHListCap : 0u, n1, n2);
+      if (lane == 0) {
+        sm.red_u[wid] = n1;
+        sm.red_v[wid] = n2;
+      }
+    }
+    __syncthreads();
+    if (wid == 0) {
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        if (which == 0 ? need1 : need2) {
+          const uint32_t jt = (uint32_t)(which == 0 ? thr_j : drw_j);
+          const uint32_t n = lane < kSW ? (which == 0 ? sm.red_u[lane] : sm.red_v[lane]) : 0u;
+          const uint32_t inc = wave_scan_u32(n), ex = inc - n;
+          if (jt >= ex && jt < inc) {
+            if (jt - ex < (uint32_t)kHListCap) {
+              sm.id_out[which] = lists[(size_t)lane * 2 * kHListCap + which * kHListCap + (jt - ex)];
+            } else {
+              sm.walk_w[which] = lane;
+              sm.walk_lo[which] = jt - ex;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (wid < 2 && sm.walk_w[wid] >= 0) {  // a list too short: wave k finds item k's member
+      int64_t r0, r1;
+      wave_range(sm.walk_w[wid], r0, r1);
+      const uint32_t lo = sm.walk_lo[wid];
+      uint32_t n1, n2;
+      collect(r0, r1, &sm.id_out[0], lo, wid == 0 ? 1u : 0u, &sm.id_out[1], lo, wid == 1 ? 1u : 0u,
+              n1, n2);
     }
   }
   __syncthreads();
