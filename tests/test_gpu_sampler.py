@@ -181,6 +181,19 @@ def test_uniform_edges_and_single_allowed():
     assert int(g_out.ids[4]) == 77777 and int(g_out.ids[5]) == V - 1
 
 
+def test_drawn_uniforms_are_randint_over_2_to_24():
+    """ops.draw_uniforms: u = randint(0, 2^24) * 2^-24 from the generator's
+    state, whichever dtype randint is asked for."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    u = ops.draw_uniforms(4099, dev, g)
+    g.manual_seed(11)
+    k = torch.randint(0, 1 << 24, (4099,), device=dev, generator=g, dtype=torch.int32)
+    assert u.dtype == torch.float32
+    assert torch.equal(u, k.to(torch.float64).mul(2.0 ** -24).to(torch.float32))
+    assert float(u.min()) >= 0.0 and float(u.max()) < 1.0
+
+
 def test_deterministic_repeat():
     wl = W.sampler_workload(5, rows=32)
     a = gpu_sample(wl.logits, **wl.kwargs())
