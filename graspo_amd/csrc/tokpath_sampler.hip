@@ -1764,7 +1764,7 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
 #pragma unroll 1
       for (int64_t s = r0; s < r1; s += (int64_t)kWave * kU) {
         u32x4 buf[kU];
-        uint32_t okw[kU], pnw[kU];
+        uint32_t okw[kU] = {}, pnw[kU] = {};
         if (vend > r0) {
 #pragma unroll
           for (int i = 0; i < kU; ++i) {
@@ -1779,6 +1779,9 @@ __device__ __forceinline__ bool hist_row(const SamplerArgs& a, int64_t b, HistSm
               pnw[i] = sm.pen[(vi < vend ? vi : vend - 1) >> 2];
             }
           }
+        } else {
+#pragma unroll
+          for (int i = 0; i < kU; ++i) buf[i] = u32x4{0u, 0u, 0u, 0u};  // no full vector in the range
         }
 #pragma unroll
         for (int i = 0; i < kU; ++i) {

@@ -85,9 +85,11 @@ def test_rows_leaving_the_histogram():
         assert_parity(gpu_sample(x, **kw), oracle_sample(x, **kw), f"rho{rho} p{p}")
 
 
-@pytest.mark.parametrize("V", [248323, 4101, 1000])
+@pytest.mark.parametrize("V", [248323, 4101, 1000, 69, 8, 7])
 def test_vocab_tail(V):
-    """Aligned rows (stride a multiple of 8) whose length is not."""
+    """Aligned rows (stride a multiple of 8) whose length is not.  V = 69
+    leaves one wave of the id pass only the partial last vector, V = 7 has
+    no full vector at all."""
     stride = (V + 7) // 8 * 8
     full, g = _rows(34, 6, stride)
     full[3] = torch.round(full[3] * 4) / 4
