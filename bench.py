@@ -10,8 +10,12 @@ sampler batches alternate and the 4 GB logprob pass between them evicts the
 
 Prints ONE JSON line.  ``value`` is sampled rows/s of the sampler kernel;
 ``logprob_tokens_per_s`` is the logprob kernel's throughput.  Kernel times
-come from HIP events recorded around each launch on the stream the kernels
-are launched on (torch's current stream, which the ops use).
+come from HIP events on the stream the kernels are launched on (torch's
+current stream, which the ops use), recorded at each kernel's own dispatch
+start and end through the library's launch hook (gtp_time_next_launch,
+hipExtLaunchKernelGGL), as rocprofv3 times a kernel.  Events recorded around
+a launch also count the event packets' idle microseconds; those figures are
+reported beside as ``avg_us_events_around_launch``.
 
 ``rooflines.logprob_backward`` times the logprob gradient kernel over the
 same [8192, 248320] logits (read once, bf16 gradient written once).
@@ -125,6 +129,20 @@ def calibrate_copy(iters: int = 5) -> None:
     print(json.dumps({"calibrate_copy_bytes": n, "iters": iters}), flush=True)
 
 
+def kernel_events(n: int):
+    """n pairs of timing events for ops.time_next_launch, each recorded once
+    so that it exists; the hook then re-records them at a kernel's own
+    dispatch start and end."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for e0, e1 in evs:
+        e0.record()
+        e1.record()
+    return evs
+
+
 def time_sampler_config(cfg: int, dev, iters: int, flush):
     """Average kernel time of one sampler launch on workload ``cfg`` with the
     MALL evicted before every launch."""
@@ -137,13 +155,11 @@ def time_sampler_config(cfg: int, dev, iters: int, flush):
     kw = wl.kwargs()
     for _ in range(2):
         ops.sample(wl.logits, **kw)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(iters)]
+    evs = kernel_events(iters)
     for e0, e1 in evs:
         flush.add_(1)
-        e0.record()
+        ops.time_next_launch(e0, e1)
         ops.sample(wl.logits, **kw)
-        e1.record()
     torch.cuda.synchronize()
     us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
     B = wl.logits.shape[0]
@@ -384,27 +400,36 @@ def main() -> int:
     torch.cuda.synchronize()
 
     def step(i, evs=None):
+        # evs: events around the two launches (0-2) and, through the launch
+        # hook, at each kernel's own start and end (3-4 sampler, 5-6 logprob)
         w = batches[i % 2]
         if evs:
             evs[0].record()
+            ops.time_next_launch(evs[3], evs[4])
         ops.sample(w.logits, **w.kwargs())
         if evs:
             evs[1].record()
+            ops.time_next_launch(evs[5], evs[6])
         ops.logprob_entropy(lx, lt)
         if evs:
             evs[2].record()
 
     for i in range(args.warmup):
         step(i)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+              + [e for pair in kernel_events(2) for e in pair] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i, events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    s_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    l_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    # kernel time: the events the launch hook records at each kernel's own
+    # dispatch; around the launches, event packets add a few idle microseconds
+    s_ms = sum(e[3].elapsed_time(e[4]) for e in events) / args.steps
+    l_ms = sum(e[5].elapsed_time(e[6]) for e in events) / args.steps
+    s_ev_us = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps * 1e3
+    l_ev_us = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps * 1e3
 
     s_bytes = wl.algorithmic_bytes()
     l_bytes = W.logprob_algorithmic_bytes(N, V, lx.element_size())
@@ -413,11 +438,11 @@ def main() -> int:
     roof_s = {"bound": "hbm", "achieved": round(s_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(s_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(SAMPLER_KERNEL),
               "kernel": SAMPLER_KERNEL, "algorithmic_bytes": s_bytes,
-              "avg_us": round(s_ms * 1e3, 2)}
+              "avg_us": round(s_ms * 1e3, 2), "avg_us_events_around_launch": round(s_ev_us, 2)}
     roof_l = {"bound": "hbm", "achieved": round(l_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(l_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(LOGPROB_KERNEL),
               "kernel": LOGPROB_KERNEL, "algorithmic_bytes": l_bytes,
-              "avg_us": round(l_ms * 1e3, 2)}
+              "avg_us": round(l_ms * 1e3, 2), "avg_us_events_around_launch": round(l_ev_us, 2)}
     dominant = roof_l if l_ms >= s_ms else roof_s
     line = {
         "metric": "sampled rows/sec and logprob tokens/sec; achieved HBM GB/s vs MI355X peak",
@@ -452,12 +477,10 @@ def main() -> int:
     grad = torch.empty_like(lx)
     for _ in range(2):
         ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
-    bevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(10)]
+    bevs = kernel_events(10)
     for e0, e1 in bevs:
-        e0.record()
+        ops.time_next_launch(e0, e1)
         ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
-        e1.record()
     torch.cuda.synchronize()
     b_ms = sum(a.elapsed_time(b) for a, b in bevs) / len(bevs)
     b_bytes = 2 * N * V * lx.element_size() + N * (lt.element_size() + 4 + 4)

@@ -6,6 +6,7 @@
 // -ffp-contract=off), so host and device produce the same integers.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -259,6 +260,25 @@ __device__ __forceinline__ void load_group(const T* row, int64_t G, int64_t V, b
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = (e0 + j < V) ? Elem<T>::get(row, e0 + j) : kNegInf;
+  }
+}
+
+// Events that the next launch through launch_timed records at its start and
+// end (hipExtLaunchKernelGGL takes them from the dispatch itself), set by
+// gtp_time_next_launch; per host thread, cleared by the launch that uses them.
+struct LaunchEvents {
+  hipEvent_t start, stop;
+};
+extern thread_local LaunchEvents g_next_launch_events;
+
+template <typename Kernel, typename... Args>
+inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
+  LaunchEvents& e = g_next_launch_events;
+  if (e.start && e.stop) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, e.start, e.stop, 0, args...);
+    e = LaunchEvents{nullptr, nullptr};
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
   }
 }
 

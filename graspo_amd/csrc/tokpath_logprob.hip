@@ -314,17 +314,17 @@ extern "C" int gtp_logprob_entropy_rows(const void* logits, int dtype, int64_t N
   const dim3 grid((unsigned)N), block(kLpBlock);
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      hipLaunchKernelGGL(logprob_entropy_kernel<uint16_t>, grid, block, 0, s,
+      launch_timed(logprob_entropy_kernel<uint16_t>, grid, block, s,
                          reinterpret_cast<const uint16_t*>(logits), V, row_stride, targets,
                          targets_int64, out_logprob, out_entropy, out_status);
       break;
     case GTP_DTYPE_F16:
-      hipLaunchKernelGGL(logprob_entropy_kernel<_Float16>, grid, block, 0, s,
+      launch_timed(logprob_entropy_kernel<_Float16>, grid, block, s,
                          reinterpret_cast<const _Float16*>(logits), V, row_stride, targets,
                          targets_int64, out_logprob, out_entropy, out_status);
       break;
     case GTP_DTYPE_F32:
-      hipLaunchKernelGGL(logprob_entropy_kernel<float>, grid, block, 0, s,
+      launch_timed(logprob_entropy_kernel<float>, grid, block, s,
                          reinterpret_cast<const float*>(logits), V, row_stride, targets,
                          targets_int64, out_logprob, out_entropy, out_status);
       break;
@@ -332,6 +332,17 @@ extern "C" int gtp_logprob_entropy_rows(const void* logits, int dtype, int64_t N
       return GTP_ERR_INVALID_ARGUMENT;
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+}
+
+namespace gtp {
+thread_local LaunchEvents g_next_launch_events{nullptr, nullptr};
+}
+
+extern "C" int gtp_time_next_launch(void* start_event, void* stop_event) {
+  if (!start_event || !stop_event) return GTP_ERR_INVALID_ARGUMENT;
+  g_next_launch_events = LaunchEvents{reinterpret_cast<hipEvent_t>(start_event),
+                                      reinterpret_cast<hipEvent_t>(stop_event)};
+  return GTP_OK;
 }
 
 extern "C" int gtp_lse_partial_rows(const void* logits, int dtype, int64_t N, int64_t Vc,
@@ -410,19 +421,19 @@ extern "C" int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t 
   const dim3 grid((unsigned)N), block(kLpBlock);
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      hipLaunchKernelGGL(logprob_backward_kernel<uint16_t>, grid, block, 0, s,
+      launch_timed(logprob_backward_kernel<uint16_t>, grid, block, s,
                          reinterpret_cast<const uint16_t*>(logits), V, row_stride, col_offset,
                          targets, targets_int64, grad_logprob, lse,
                          reinterpret_cast<uint16_t*>(grad), grad_stride);
       break;
     case GTP_DTYPE_F16:
-      hipLaunchKernelGGL(logprob_backward_kernel<_Float16>, grid, block, 0, s,
+      launch_timed(logprob_backward_kernel<_Float16>, grid, block, s,
                          reinterpret_cast<const _Float16*>(logits), V, row_stride, col_offset,
                          targets, targets_int64, grad_logprob, lse,
                          reinterpret_cast<_Float16*>(grad), grad_stride);
       break;
     case GTP_DTYPE_F32:
-      hipLaunchKernelGGL(logprob_backward_kernel<float>, grid, block, 0, s,
+      launch_timed(logprob_backward_kernel<float>, grid, block, s,
                          reinterpret_cast<const float*>(logits), V, row_stride, col_offset,
                          targets, targets_int64, grad_logprob, lse,
                          reinterpret_cast<float*>(grad), grad_stride);

@@ -1930,20 +1930,20 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&
       a.hist_len <= 65535) {
     if (a.mask)
-      hipLaunchKernelGGL((sampler_hist_kernel<uint16_t, true>), grid, block, 0, s, a);
+      launch_timed(sampler_hist_kernel<uint16_t, true>, grid, block, s, a);
     else
-      hipLaunchKernelGGL((sampler_hist_kernel<uint16_t, false>), grid, block, 0, s, a);
+      launch_timed(sampler_hist_kernel<uint16_t, false>, grid, block, s, a);
     return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
   }
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      hipLaunchKernelGGL(sampler_rowwise_kernel<uint16_t>, grid, block, 0, s, a);
+      launch_timed(sampler_rowwise_kernel<uint16_t>, grid, block, s, a);
       break;
     case GTP_DTYPE_F16:
-      hipLaunchKernelGGL(sampler_rowwise_kernel<_Float16>, grid, block, 0, s, a);
+      launch_timed(sampler_rowwise_kernel<_Float16>, grid, block, s, a);
       break;
     case GTP_DTYPE_F32:
-      hipLaunchKernelGGL(sampler_rowwise_kernel<float>, grid, block, 0, s, a);
+      launch_timed(sampler_rowwise_kernel<float>, grid, block, s, a);
       break;
     default:
       return GTP_ERR_INVALID_ARGUMENT;

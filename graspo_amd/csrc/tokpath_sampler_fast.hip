@@ -1449,16 +1449,16 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
   const bool m = allow_mask != nullptr;
   switch (dtype) {
     case GTP_DTYPE_BF16:
-      if (m) hipLaunchKernelGGL((sampler_split_kernel<uint16_t, true>), grid, block, 0, st, fa);
-      else hipLaunchKernelGGL((sampler_split_kernel<uint16_t, false>), grid, block, 0, st, fa);
+      if (m) launch_timed(sampler_split_kernel<uint16_t, true>, grid, block, st, fa);
+      else launch_timed(sampler_split_kernel<uint16_t, false>, grid, block, st, fa);
       break;
     case GTP_DTYPE_F16:
-      if (m) hipLaunchKernelGGL((sampler_split_kernel<_Float16, true>), grid, block, 0, st, fa);
-      else hipLaunchKernelGGL((sampler_split_kernel<_Float16, false>), grid, block, 0, st, fa);
+      if (m) launch_timed(sampler_split_kernel<_Float16, true>, grid, block, st, fa);
+      else launch_timed(sampler_split_kernel<_Float16, false>, grid, block, st, fa);
       break;
     default:
-      if (m) hipLaunchKernelGGL((sampler_split_kernel<float, true>), grid, block, 0, st, fa);
-      else hipLaunchKernelGGL((sampler_split_kernel<float, false>), grid, block, 0, st, fa);
+      if (m) launch_timed(sampler_split_kernel<float, true>, grid, block, st, fa);
+      else launch_timed(sampler_split_kernel<float, false>, grid, block, st, fa);
       break;
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;

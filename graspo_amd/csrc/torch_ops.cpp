@@ -1,7 +1,7 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
-// lse_finalize, decode_update, to_bf16_exact, logprob_backward_split}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lse_finalize, decode_update, to_bf16_exact, logprob_backward_split, time_next_launch}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -424,6 +424,14 @@ std::tuple<at::Tensor, at::Tensor> to_bf16_exact(const at::Tensor& src, int64_t 
 
 }  // namespace
 
+void time_next_launch(int64_t start_event, int64_t stop_event) {
+  TORCH_CHECK(start_event != 0 && stop_event != 0,
+              "graspo_tokpath.time_next_launch: both events must exist (record them once first)");
+  check_rc(gtp_time_next_launch(reinterpret_cast<void*>(start_event),
+                                reinterpret_cast<void*>(stop_event)),
+           "gtp_time_next_launch");
+}
+
 TORCH_LIBRARY(graspo_tokpath, m) {
   m.def(
       "sample(Tensor logits, float temperature, int top_k, float top_p, float repetition_penalty, "
@@ -456,6 +464,7 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "Tensor(d!) flags, int stream) -> ()",
       &decode_update);
   m.def("to_bf16_exact(Tensor src, int stream) -> (Tensor, Tensor)", &to_bf16_exact);
+  m.def("time_next_launch(int start_event, int stop_event) -> ()", &time_next_launch);
   m.def(
       "logprob_backward_split(Tensor logits, Tensor targets, Tensor grad_logprob, Tensor lse, "
       "int col_offset, int stream) -> (Tensor, Tensor)",

@@ -193,6 +193,15 @@ def to_bf16_exact(src: torch.Tensor):
     return ops.to_bf16_exact(src.contiguous(), _stream(src))
 
 
+def time_next_launch(start: torch.cuda.Event, stop: torch.cuda.Event) -> None:
+    """Measurement hook: the next sampler, logprob or logprob-gradient kernel
+    launched from this thread records ``start`` and ``stop`` (timing events
+    that have been recorded once, so that they exist) at its own dispatch's
+    start and end."""
+    ops = load()
+    ops.time_next_launch(int(start.cuda_event), int(stop.cuda_event))
+
+
 def new_lse_state(rows: int, device) -> torch.Tensor:
     return torch.empty((rows, 4), dtype=torch.float32, device=device)
 

@@ -303,6 +303,17 @@ int gtp_decode_update_rows(const int64_t* ids, const int32_t* status, int64_t B,
 int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
                           uint32_t* inexact, void* stream);
 
+/*
+ * gtp_time_next_launch -- measurement hook, no counterpart in the reference:
+ * the next gtp_sample_rows, gtp_logprob_entropy_rows or
+ * gtp_logprob_backward_rows kernel launched from the calling thread records start_event when its dispatch begins and
+ * stop_event when it ends (hipExtLaunchKernelGGL), so the two HIP events
+ * bracket the kernel alone, without the idle time of event packets recorded
+ * around it.  Both are hipEvent_t created by the caller (with timing).  The
+ * hook is per thread and used once; the benchmark is its caller.
+ */
+int gtp_time_next_launch(void* start_event, void* stop_event);
+
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
 
