@@ -55,6 +55,10 @@ def test_dense_value_bins(top_p, top_k):
 def test_penalty_and_mask(rho):
     x, g = _rows(32, 8, V_LARGE, 2.5)
     x[1] = torch.round(x[1] * 8) / 8
+    # one or two values: a wave of the id pass holds thousands of members of
+    # a bin, past its 512-entry list, with the mask and the penalty applied
+    x[2] = 1.0
+    x[3] = (torch.arange(V_LARGE) % 2).float() * 0.5 + 1.0
     x = x.to(torch.bfloat16)
     hist = torch.randint(-1, V_LARGE, (8, 300), generator=g, dtype=torch.int32)
     bits = torch.rand(8, V_LARGE, generator=g) < 0.3
