@@ -53,17 +53,21 @@ def _run(cmd: list[str]) -> None:
 
 def build_hip(verbose: bool = False) -> str:
     """Compile the HIP sources into libgraspo_tokpath.so (always rebuilds)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     hipcc = _hipcc()
-    objs = []
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
+    cmds, objs = [], []
     for src in HIP_SOURCES:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-        cmd = [hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
-        if verbose:
-            print(" ".join(cmd))
-        _run(cmd)
+        cmds.append([hipcc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
+        if verbose:
+            print(" ".join(cmds[-1]))
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(_run, cmds))
     tmp = LIB_PATH + ".tmp"
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB_PATH)

@@ -13,6 +13,10 @@
 // updates `finished` in place and writes two counters (rows still
 // unfinished, rows whose sampler status is not OK) that the host reads
 // asynchronously, a step later, instead of synchronising on every token.
+// A row whose sampler status is not OK carries id -1; its id is replaced by
+// pad_token_id here (in `ids` itself, in the sequence and in the attention
+// mask) so that the next forward, queued before the host reads the counts
+// and raises, never embeds an id outside [0, V).
 #include "tokpath_common.h"
 
 namespace gtp {
@@ -20,19 +24,24 @@ namespace gtp {
 constexpr int kDuBlock = 1024;
 
 __global__ __launch_bounds__(kDuBlock) void decode_update_kernel(
-    const int64_t* __restrict__ ids, const int32_t* __restrict__ status, int64_t B, int64_t eos,
+    int64_t* __restrict__ ids, const int32_t* __restrict__ status, int64_t B, int64_t eos,
     int64_t pad, uint8_t* __restrict__ finished, int64_t* __restrict__ seq, int64_t seq_stride,
     uint8_t* __restrict__ attn, int64_t attn_stride, int64_t col, int32_t* __restrict__ flags) {
   __shared__ int32_t red[2][kDuBlock / kWave];
   int32_t open = 0, bad = 0;
   for (int64_t b = threadIdx.x; b < B; b += kDuBlock) {
-    const int64_t id = ids[b];
+    const bool row_bad = status && status[b] != GTP_ROW_OK;
+    int64_t id = ids[b];
+    if (row_bad) {
+      id = pad;
+      ids[b] = pad;
+    }
     const bool f = finished[b] != 0 || id == eos;
     finished[b] = f ? 1 : 0;
     if (seq) seq[b * seq_stride + col] = id;
     if (attn) attn[b * attn_stride + col] = id != pad ? 1 : 0;
     open += f ? 0 : 1;
-    bad += (status && status[b] != GTP_ROW_OK) ? 1 : 0;
+    bad += row_bad ? 1 : 0;
   }
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -61,7 +70,7 @@ __global__ __launch_bounds__(kDuBlock) void decode_update_kernel(
 
 using namespace gtp;
 
-extern "C" int gtp_decode_update_rows(const int64_t* ids, const int32_t* status, int64_t B,
+extern "C" int gtp_decode_update_rows(int64_t* ids, const int32_t* status, int64_t B,
                                       int64_t eos_token_id, int64_t pad_token_id,
                                       uint8_t* finished, int64_t* seq, int64_t seq_stride,
                                       uint8_t* attn, int64_t attn_stride, int64_t col,

@@ -13,6 +13,13 @@
 // with dl/dlogp = -A r where the minimum takes r A or r lies inside the
 // clip range (torch's min splits a tie in halves of equal value, and
 // clamp passes the gradient on its closed range), else 0.
+//
+// Non-finite values follow torch: min and clamp pass NaN through (fminf
+// and fmaxf would drop it), a masked position still multiplies its loss by
+// the mask (NaN * 0 = NaN poisons the sum, as (tensor * mask).sum() does),
+// and the gradient is formed in autograd's order -- the minimum's gradient
+// goes to both operands when they are unordered, clamp's to neither -- so
+// a NaN or an inf reaches the same gradient positions.
 #include "tokpath_common.h"
 
 namespace gtp {
@@ -30,6 +37,15 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
   for (int w = 0; w < kLsBlock / kWave; ++w) s += red[w];
   __syncthreads();
   return s;
+}
+
+// torch.minimum: NaN if either operand is NaN
+__device__ __forceinline__ float min_nan(float a, float b) {
+  return (a != a || b != b) ? a + b : (a < b ? a : b);
+}
+// torch.clamp(r, lo, hi) with finite bounds: NaN stays NaN
+__device__ __forceinline__ float clamp_nan(float r, float lo, float hi) {
+  return r != r ? r : fminf(fmaxf(r, lo), hi);
 }
 
 // action mask: fp32 weights, bytes (bool, 0 or 1), or none (all ones)
@@ -56,8 +72,8 @@ __global__ __launch_bounds__(kLsBlock) void graspo_loss_rows_kernel(
     const float r = expf(logp[i] - old_logp[i]);
     const float A = adv[i];
     const float s1 = r * A;
-    const float s2 = fminf(fmaxf(r, lo), hi) * A;
-    s += -fminf(s1, s2) * m;
+    const float s2 = clamp_nan(r, lo, hi) * A;
+    s += -min_nan(s1, s2) * m;
     d += m;
   }
   s = block_sum_256(s, red);
@@ -91,10 +107,17 @@ __global__ __launch_bounds__(kLsBlock) void graspo_loss_backward_kernel(
   const float r = expf(logp[n] - old_logp[n]);
   const float A = adv[n];
   const float s1 = r * A;
-  const float s2 = fminf(fmaxf(r, lo), hi) * A;
-  const bool pass = s1 <= s2 || (r >= lo && r <= hi);
-  const float c = grad_loss[0] / (float)B * inv_denom[b] * m;
-  grad_logp[n] = pass ? -A * r * c : 0.0f;
+  const float s2 = clamp_nan(r, lo, hi) * A;
+  // d loss_bt: the mean over sequences, the masked mean and the negation
+  const float gl = -(grad_loss[0] / (float)B * inv_denom[b] * m);
+  // torch.minimum's backward: all to the smaller operand, halves on a tie,
+  // the whole to both when the comparison is unordered (a NaN)
+  float w1 = 1.0f, w2 = 1.0f;
+  if (s1 < s2) w2 = 0.0f;
+  else if (s1 > s2) w1 = 0.0f;
+  else if (s1 == s2) w1 = w2 = 0.5f;
+  const float g2 = (r >= lo && r <= hi) ? (w2 * gl) * A : 0.0f;  // clamp passes [lo, hi]
+  grad_logp[n] = ((w1 * gl) * A + g2) * r;                        // exp's backward: * r
 }
 
 }  // namespace gtp

@@ -468,12 +468,23 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   const float lse_m = row_lse.m, lse_ln = __builtin_amdgcn_logf(row_lse.s) * kLn2;
   const bool nonfinite = (row_lse.s != row_lse.s) || row_lse.m == kPosInf;
 
+  // A row without an answer on the ordered paths (block-uniform call):
+  // greedy rows take the argmax semantics of greedy_argmax_rescan (wave 0
+  // scans the row; sm.pen already holds the penalised ids), other rows
+  // report `st`.
+  auto fail = [&](int32_t st) __attribute__((always_inline)) {
+    if (r.greedy && !bad_hist) {
+      if (tid < kWave) greedy_argmax_rescan<T>(a, b, sm.pen, false, nonfinite, lse_m, lse_ln);
+      return;
+    }
+    if (tid == 0) write_row(a, b, r.greedy ? GTP_ROW_BAD_HISTORY : st, -1, 0.f, 0.f, 0, 0.f, -1);
+  };
   int32_t status = GTP_ROW_OK;
   if (nonfinite) status = GTP_ROW_NONFINITE;
   else if (bad_hist) status = GTP_ROW_BAD_HISTORY;
   else if (!r.greedy && !(u >= 0.0f && u < 1.0f)) status = GTP_ROW_BAD_UNIFORM;
   if (status != GTP_ROW_OK) {
-    if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
+    fail(status);
     return;
   }
 
@@ -553,7 +564,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     if (nc > kCandCap) {
       general = true;
     } else if (nc == 0) {
-      if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
+      fail(GTP_ROW_EMPTY);
       return;
     } else {
       const int nk = Keff < nc ? Keff : nc;
@@ -568,7 +579,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
       const unsigned long long k0 = sm.cand_key[sm.order[0]];
       const float m = rank_key_y(k0);
       if (m == kPosInf) {
-        if (tid == 0) write_row(a, b, GTP_ROW_NONFINITE, -1, 0.f, 0.f, 0, 0.f, -1);
+        fail(GTP_ROW_NONFINITE);
         return;
       }
       if (r.greedy) {
@@ -640,11 +651,11 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   for_each_valid<T>(r, sm, [&](int32_t, float y, float) { ymax = fmaxf(ymax, y); });
   const float m = block_max(sm, ymax);
   if (m == kNegInf) {
-    if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
+    fail(GTP_ROW_EMPTY);
     return;
   }
   if (m == kPosInf) {
-    if (tid == 0) write_row(a, b, GTP_ROW_NONFINITE, -1, 0.f, 0.f, 0, 0.f, -1);
+    fail(GTP_ROW_NONFINITE);
     return;
   }
   GeneralSmem& g = sm.u.gen;

@@ -48,6 +48,9 @@
 //
 // Replaces _next_token_from_logits / _sample_next_token
 // (src/graspo/backends/graspoflow/tensor_utils.py:649-683).
+#include <atomic>
+#include <mutex>
+
 #include "tokpath_sampler_internal.h"
 #include "tokpath_stream.h"
 
@@ -562,7 +565,8 @@ __device__ __forceinline__ void select_top_slow(FastSmem& sm, const Slice<T>& c,
 // or fixed-point top-p cut and draw, outputs.  Wave 0 only (lane r/2 holds
 // the weights of ranks r); the cut and the draw are counts of prefix sums
 // below a bound, taken with ballots.  Callers sync before (lists complete).
-__device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& fa, int64_t b,
+template <typename T>
+__device__ __forceinline__ void finish_row(FastSmem& sm, const FastArgs& fa, int64_t b,
                                            float u, float lm, float ls, bool bad_hist,
                                            uint32_t nk) {
   const SamplerArgs& a = fa.a;
@@ -570,8 +574,9 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   if (lane >= kWave) return;
   // logprob = x - m - ln s, rounded once (raw_logprob)
   const float lse_m = lm, lse_ln = __builtin_amdgcn_logf(ls) * kLn2;
+  const bool raw_nonfinite = ls != ls || lm == kPosInf;
   int32_t status = GTP_ROW_OK;
-  if (ls != ls || lm == kPosInf)
+  if (raw_nonfinite)
     status = GTP_ROW_NONFINITE;
   else if (bad_hist)
     status = GTP_ROW_BAD_HISTORY;
@@ -582,6 +587,11 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
   else if (rank_key_y(sm.fkey[0]) == kPosInf)
     status = GTP_ROW_NONFINITE;
   if (status != GTP_ROW_OK) {
+    if (fa.greedy && !bad_hist) {  // argmax semantics for NaN, +inf and all -inf rows
+      greedy_argmax_rescan<T>(a, b, sm.pen, true, raw_nonfinite, lse_m, lse_ln);
+      return;
+    }
+    if (fa.greedy) status = GTP_ROW_BAD_HISTORY;
     if (lane == 0) write_out(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
     return;
   }
@@ -629,6 +639,7 @@ __device__ __forceinline__ void finish_row(const FastSmem& sm, const FastArgs& f
 
 // The last workgroup of a split row: gather the S sorted lists, rank the
 // union by binary search, finish.  Block-uniform.
+template <typename T>
 __device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int64_t b, float u,
                                           int S) {
   const int tid = threadIdx.x;
@@ -693,7 +704,7 @@ __device__ __forceinline__ void merge_row(FastSmem& sm, const FastArgs& fa, int6
     }
   }
   __syncthreads();
-  finish_row(sm, fa, b, u, lm, ls, any_bad_hist, nk);
+  finish_row<T>(sm, fa, b, u, lm, ls, any_bad_hist, nk);
 }
 
 // --------------------------------------------------------------- the kernel
@@ -1275,7 +1286,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
     if (tid >= kWave) return;
     float lm, ls;
     merged_lse(lm, ls);
-    finish_row(sm, fa, b, u_row, lm, ls, bad_hist, nout);
+    finish_row<T>(sm, fa, b, u_row, lm, ls, bad_hist, nout);
     return;
   }
   if (tid < kWave) {
@@ -1310,7 +1321,7 @@ __global__ __launch_bounds__(kFT) void sampler_split_kernel(FastArgs fa) {
   }
   __syncthreads();
   if (!sm.flag) return;
-  merge_row(sm, fa, b, u_row, S);
+  merge_row<T>(sm, fa, b, u_row, S);
 }
 
 // ------------------------------------------------------------------ planning
@@ -1328,17 +1339,18 @@ int elem_size(int dtype) { return dtype == GTP_DTYPE_F32 ? 4 : 2; }
 // Compute units of the current device (cached per device): the launch aims
 // at one resident workgroup per CU so that every slice streams at once and
 // the selection tails run after the memory system has drained.
+// Threads that race on a device's first call both store the same value.
 int64_t device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, bool aligned) {
@@ -1382,6 +1394,22 @@ extern "C" size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
   return pl.fast ? pl.ws_bytes : 0;
 }
 
+namespace gtp {
+
+// gtp_sample_rows with its workspace; `clear_counters` zeroes the per-row
+// arrival counters first (a fill kernel, so a captured graph holds no memset
+// node), for a workspace whose previous contents the call cannot vouch for.
+int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                     const int32_t* history, int64_t hist_len, int64_t hist_stride,
+                     const uint32_t* allow_mask, int64_t mask_stride, const float* uniforms,
+                     const gtp_sampler_params* params, const uint8_t* finished,
+                     int64_t pad_token_id, int64_t* out_ids, float* out_logprob,
+                     float* out_sampled_logprob, int32_t* out_kept, float* out_thresh_value,
+                     int32_t* out_thresh_id, int32_t* out_status, void* workspace,
+                     size_t workspace_bytes, bool clear_counters, void* stream);
+
+}  // namespace gtp
+
 extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
                                int64_t row_stride, const int32_t* history, int64_t hist_len,
                                int64_t hist_stride, const uint32_t* allow_mask, int64_t mask_stride,
@@ -1390,6 +1418,27 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
                                float* out_logprob, float* out_sampled_logprob, int32_t* out_kept,
                                float* out_thresh_value, int32_t* out_thresh_id, int32_t* out_status,
                                void* workspace, size_t workspace_bytes, void* stream) {
+  return sample_rows_impl(logits, dtype, B, V, row_stride, history, hist_len, hist_stride,
+                          allow_mask, mask_stride, uniforms, params, finished, pad_token_id,
+                          out_ids, out_logprob, out_sampled_logprob, out_kept, out_thresh_value,
+                          out_thresh_id, out_status, workspace, workspace_bytes, false, stream);
+}
+
+namespace gtp {
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                     const int32_t* history, int64_t hist_len, int64_t hist_stride,
+                     const uint32_t* allow_mask, int64_t mask_stride, const float* uniforms,
+                     const gtp_sampler_params* params, const uint8_t* finished,
+                     int64_t pad_token_id, int64_t* out_ids, float* out_logprob,
+                     float* out_sampled_logprob, int32_t* out_kept, float* out_thresh_value,
+                     int32_t* out_thresh_id, int32_t* out_status, void* workspace,
+                     size_t workspace_bytes, bool clear_counters, void* stream) {
   if (!params || B < 0 || V <= 0 || row_stride < V) return GTP_ERR_INVALID_ARGUMENT;
   if (dtype != GTP_DTYPE_F32 && dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F16)
     return GTP_ERR_INVALID_ARGUMENT;
@@ -1434,6 +1483,11 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
   if (!pl.fast) return launch_sampler_general(a, dtype, B, st);
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes))
     return GTP_ERR_INVALID_ARGUMENT;
+  if (clear_counters && pl.ws_bytes > 0) {
+    const int64_t nw = (int64_t)(pl.cnt_bytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<uint32_t*>(workspace), nw);
+  }
 
   FastArgs fa;
   fa.a = a;
@@ -1463,3 +1517,5 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }
+
+}  // namespace gtp

@@ -459,7 +459,7 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "int stream) -> Tensor",
       &graspo_loss_backward);
   m.def(
-      "decode_update(Tensor ids, Tensor? status, Tensor(a!) finished, int eos_token_id, "
+      "decode_update(Tensor(e!) ids, Tensor? status, Tensor(a!) finished, int eos_token_id, "
       "int pad_token_id, Tensor(b!)? sequences, Tensor(c!)? attention_mask, int col, "
       "Tensor(d!) flags, int stream) -> ()",
       &decode_update);

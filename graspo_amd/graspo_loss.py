@@ -14,9 +14,10 @@ from torch import nn
 from . import ops
 
 
-def _rows_logprob_entropy(logits: torch.Tensor, output_ids: torch.Tensor):
-    """(logprob, entropy) over the last dim of ``logits`` [..., V]; views whose
-    leading dims cannot be flattened without a copy are walked per slice."""
+def _rows_logprob_entropy_status(logits: torch.Tensor, output_ids: torch.Tensor):
+    """(logprob, entropy, status) over the last dim of ``logits`` [..., V];
+    views whose leading dims cannot be flattened without a copy are walked
+    per slice."""
     V = logits.shape[-1]
     lead = logits.shape[:-1]
     if logits.stride(-1) != 1:
@@ -26,14 +27,20 @@ def _rows_logprob_entropy(logits: torch.Tensor, output_ids: torch.Tensor):
     except RuntimeError:
         rows = None
     if rows is not None:
-        lp, H, _ = ops.logprob_entropy(rows, output_ids.reshape(-1))
-        return lp.view(lead), H.view(lead)
-    lps, Hs = [], []
-    for i in range(logits.shape[0]):
-        lp_i, H_i = _rows_logprob_entropy(logits[i], output_ids[i])
-        lps.append(lp_i)
-        Hs.append(H_i)
-    return torch.stack(lps), torch.stack(Hs)
+        lp, H, st = ops.logprob_entropy(rows, output_ids.reshape(-1))
+        return lp.view(lead), H.view(lead), st.view(lead)
+    parts = [_rows_logprob_entropy_status(logits[i], output_ids[i])
+             for i in range(logits.shape[0])]
+    return tuple(torch.stack(p) for p in zip(*parts))
+
+
+def _rows_logprob_entropy(logits: torch.Tensor, output_ids: torch.Tensor):
+    """(logprob, entropy); a target outside [0, V) raises ``RuntimeError``, as
+    the reference's ``gather`` rejects such an index (one host
+    synchronisation on the per-row status)."""
+    lp, H, st = _rows_logprob_entropy_status(logits, output_ids)
+    ops.raise_on_bad_status(st.reshape(-1), "sequence_log_probs_from_logits")
+    return lp, H
 
 
 class _SequenceLogProbs(torch.autograd.Function):

@@ -179,7 +179,8 @@ def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torc
     """After a sampler step: ``sequences[:, col] = ids``,
     ``attention_mask[:, col] = ids != pad``, ``finished |= ids == eos`` (in
     place) and ``flags = [rows still unfinished, rows with a bad status]``
-    (int32 [2]), in one launch."""
+    (int32 [2]), in one launch.  Rows with a bad status get ``pad_token_id``
+    in ``ids`` (in place) as well as in the two columns."""
     ops = load()
     ops.decode_update(ids, status, finished, int(eos_token_id), int(pad_token_id), sequences,
                       attention_mask, int(col), flags, _stream(ids))

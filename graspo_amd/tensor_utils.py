@@ -146,6 +146,10 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         h2 = hidden.reshape(-1, H)
         t = output_ids.reshape(-1)
         N, V = h2.shape[0], weight.shape[0]
+        # the reference's index_select / gather rejects an id outside [0, V)
+        if N and bool(((t < 0) | (t >= V)).any()):
+            raise RuntimeError(
+                "_selected_token_log_probs_from_hidden: an output id is outside [0, vocab_size)")
         mc = _matrix_core_operands(h2, weight)
         state = ops.new_lse_state(N, hidden.device)
         # (running each chunk's lse on a second stream beside the next GEMM

@@ -13,7 +13,10 @@
  *
  * Conventions shared by every entry point:
  *   - All array pointers are DEVICE pointers owned by the caller.  The library
- *     never allocates, keeps no mutable global state and is reentrant.
+ *     never allocates and is reentrant.  Its only mutable global state is:
+ *     the measurement hook's per-thread event pair (gtp_time_next_launch);
+ *     and a per-device cache of the compute-unit count, filled once per
+ *     device with atomic stores.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL is the default stream).
  *   - Return value: GTP_OK or a GTP_ERR_* code for a bad argument or a failed
@@ -32,6 +35,12 @@
  *   valid = { i : allowed_i and y_i > -inf };  empty -> status EMPTY
  *   order = (y desc, id asc); NONFINITE if the largest y is +inf
  *   T <= 0 (greedy): id = first in order; kept = 1; sampled_logprob = 0.
+ *          Greedy is torch's argmax (tensor_utils.py:658) over the allowed
+ *          tokens' y: a NaN beats every value and +inf every finite one
+ *          (first by id), and allowed tokens that are all -inf give the
+ *          first of them.  Such rows are GTP_ROW_OK, with logprob NaN when
+ *          the raw row holds a NaN or +inf; only no allowed token at all
+ *          (EMPTY) or a bad history id fails a greedy row.
  *   top-k: if 0 < K < |valid| keep the first K, else keep all valid.
  *   m = y of the first in order; w_i = DETEXP_FIX(y_i - m) (uint64, 2^40 = 1.0)
  *   top-p: if 0 < P < 1, with W = sum of kept w and S_r = sum_{j<r} w_j,
@@ -270,8 +279,11 @@ int gtp_graspo_loss_backward(const float* logp, const float* old_logp,
  * (sequences = cat([sequences, next_token]); finished |= next_token == eos;
  * all_finished = bool(finished.all()); attention_mask = sequences.ne(pad)).
  *
- *   ids       [B] int64, the sampler's out_ids (rows finished before the
- *             step already hold pad_token_id)
+ *   ids       [B] int64 in/out, the sampler's out_ids (rows finished before
+ *             the step already hold pad_token_id).  A row whose status is
+ *             not GTP_ROW_OK (its id is -1) gets pad_token_id here, in ids,
+ *             seq and attn alike, so no id outside [0, V) reaches the next
+ *             forward before the caller reads flags[1] and raises.
  *   status    [B] int32, the sampler's out_status, or NULL
  *   finished  [B] uint8 (or bool) in/out: finished[b] |= ids[b] == eos_token_id
  *   seq       [B, seq_stride] int64 or NULL: seq[b, col] = ids[b]
@@ -282,7 +294,7 @@ int gtp_graspo_loss_backward(const float* logp, const float* old_logp,
  *             host memory asynchronously; flags[0] == 0 is the reference's
  *             all_finished.
  */
-int gtp_decode_update_rows(const int64_t* ids, const int32_t* status, int64_t B,
+int gtp_decode_update_rows(int64_t* ids, const int32_t* status, int64_t B,
                            int64_t eos_token_id, int64_t pad_token_id,
                            uint8_t* finished, int64_t* seq, int64_t seq_stride,
                            uint8_t* attn, int64_t attn_stride, int64_t col,

@@ -248,8 +248,15 @@ def sample_semantic(
         if temperature > 0:
             row = row / np.float32(max(float(temperature), 1e-6))  # tensor_utils.py:656
         else:
-            masked = torch.where(torch.from_numpy(allowed[b]), row, torch.tensor(-np.inf))
-            out.append((int(torch.argmax(masked)), 1, np.inf, np.inf))  # tensor_utils.py:658
+            allow = torch.from_numpy(allowed[b])
+            if not bool(allow.any()):
+                out.append((-1, 0, np.inf, np.inf))
+                continue
+            masked = torch.where(allow, row, torch.tensor(-np.inf))
+            gid = int(torch.argmax(masked))  # tensor_utils.py:658 (NaN, then +inf, win)
+            if not bool(allow[gid]):  # every allowed token is -inf: the first of them
+                gid = int(allow.nonzero()[0])
+            out.append((gid, 1, np.inf, np.inf))
             continue
         y = row.double()
         y = torch.where(torch.from_numpy(allowed[b]), y, torch.tensor(-np.inf, dtype=torch.float64))

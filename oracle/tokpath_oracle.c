@@ -245,6 +245,49 @@ int gtp_oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
     }
     const float u = greedy ? 0.0f : uniforms[b];
     int32_t status = GTP_ROW_OK;
+    if (greedy) {
+      /* T <= 0 is the reference's logits.argmax(dim=-1) (tensor_utils.py:658)
+       * over the allowed tokens' penalised logits: a NaN beats every value
+       * and +inf every finite one (torch's argmax propagates NaN), ties go
+       * to the lowest id, and a row whose allowed tokens are all -inf
+       * returns the first of them.  Only a row with no allowed token at all
+       * (or a bad history id) has no answer. */
+      if (bad_hist) {
+        write_bad_row(b, GTP_ROW_BAD_HISTORY, finished, pad_token_id, out_ids, out_logprob,
+                      out_sampled_logprob, out_kept, out_thresh_value, out_thresh_id,
+                      out_status);
+        continue;
+      }
+      int64_t best = -1;
+      float by = 0.0f;
+      for (int64_t i = 0; i < V; ++i) {
+        if (allow_mask && !((allow_mask[b * mask_stride + (i >> 5)] >> (i & 31)) & 1u))
+          continue;
+        const float x = load_x(logits, dtype, base + i);
+        float y = x;
+        if (use_pen && pen[i]) y = (x < 0.0f) ? x * rho : x / rho;
+        y = y + 0.0f;
+        if (best < 0 || (!isnan(by) && (isnan(y) || y > by))) {
+          best = i;
+          by = y;
+        }
+      }
+      if (best < 0) {
+        write_bad_row(b, GTP_ROW_EMPTY, finished, pad_token_id, out_ids, out_logprob,
+                      out_sampled_logprob, out_kept, out_thresh_value, out_thresh_id,
+                      out_status);
+        continue;
+      }
+      const double xb = load_x(logits, dtype, base + best);
+      out_ids[b] = (finished && finished[b]) ? pad_token_id : best;
+      if (out_logprob) out_logprob[b] = nonfinite ? NAN : (float)(xb - M - log(S));
+      if (out_sampled_logprob) out_sampled_logprob[b] = 0.0f;
+      if (out_kept) out_kept[b] = 1;
+      if (out_thresh_value) out_thresh_value[b] = by;
+      if (out_thresh_id) out_thresh_id[b] = (int32_t)best;
+      if (out_status) out_status[b] = GTP_ROW_OK;
+      continue;
+    }
     if (nonfinite) status = GTP_ROW_NONFINITE;
     else if (bad_hist) status = GTP_ROW_BAD_HISTORY;
     else if (!greedy && !(u >= 0.0f && u < 1.0f)) status = GTP_ROW_BAD_UNIFORM;

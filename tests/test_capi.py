@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -168,3 +169,130 @@ def test_decode_loop_has_no_cpu_path():
         graspo_amd.load().decode_update(torch.zeros(2, dtype=torch.int64), None,
                                         torch.zeros(2, dtype=torch.bool), 1, 0, None, None, 0,
                                         torch.zeros(2, dtype=torch.int32), 0)
+
+
+def _device_case(case, dev):
+    """(logits, kwargs) of one raw-ABI sampler case, on the device."""
+    from graspo_amd import workloads as W
+
+    kind = case[0]
+    if kind == "workload":
+        wl = W.sampler_workload(case[1], rows=case[2])
+        kw = wl.kwargs()
+        kw.update(case[3])
+        return wl.logits.to(dev), {k: (v.to(dev) if isinstance(v, torch.Tensor) else v)
+                                   for k, v in kw.items()}
+    _, B, V, dtype, params, seed = case
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, V, generator=g) * 2.5).to(dtype)
+    u = ((torch.randint(0, 1 << 24, (B,), generator=g).float()) * 2.0 ** -24)
+    return x.to(dev), dict(params, uniforms=u.to(dev))
+
+
+# Calls in a row on one caller-owned workspace: B, V, dtype and top-k all
+# change from call to call (split rows with S > 1, one-slice rows, greedy,
+# and the one-workgroup paths that need no workspace).
+RAW_CASES = [
+    ("workload", 2, 64, dict(top_k=50)),                            # bf16, S = 4
+    ("workload", 1, 8, {}),                                         # fp32 [8, 151936], k 50
+    ("rand", 3, 40000, torch.bfloat16, dict(temperature=0.0), 1),   # greedy
+    ("workload", 5, 256, {}),                                       # the large batch, S = 1
+    ("rand", 17, 151936, torch.bfloat16, dict(temperature=0.8, top_k=128), 2),
+    ("workload", 3, 64, {}),                                        # top-p only: no workspace
+    ("rand", 64, 151936, torch.float32, dict(temperature=1.0, top_k=9, top_p=0.5), 3),
+]
+
+
+@pytest.mark.gpu
+def test_raw_abi_sampler_calls_share_one_workspace():
+    """gtp_sample_rows through ctypes on caller-owned device buffers, as a
+    non-torch caller binds it: one workspace sized by
+    gtp_sample_workspace_bytes over every call, zero-filled once, then
+    reused by calls whose B, V, dtype and top-k change.  Each call is
+    bit-exact against the oracle (ids, kept, threshold, status)."""
+    from tests import _capi
+    from tests._util import oracle_sample
+
+    L = _capi.lib()
+    dev = torch.device("cuda:0")
+    cases = [_device_case(c, dev) for c in RAW_CASES]
+    need = 0
+    for x, kw in cases:
+        _, p, B = _capi.sample_args(x, **kw)
+        need = max(need, L.gtp_sample_workspace_bytes(_capi.DTYPE[x.dtype], B, x.shape[1],
+                                                      ctypes.byref(p)))
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)  # zero-filled once
+    for i, (x, kw) in enumerate(cases):
+        print("raw abi sampler call", i, RAW_CASES[i][:3], flush=True)
+        args, p, B = _capi.sample_args(x, **kw)
+        out = _capi.SampleBuffers(B, dev)
+        rc = L.gtp_sample_rows(*args, *out.out_args(), ws.data_ptr(), need,
+                               _capi.stream_handle())
+        assert rc == 0
+        torch.cuda.synchronize()
+        got = out.cpu()
+        ref = oracle_sample(x.cpu(), **{k: (v.cpu() if isinstance(v, torch.Tensor) else v)
+                                        for k, v in kw.items()})
+        assert np.array_equal(got["status"].numpy(), ref.status), i
+        assert np.array_equal(got["ids"].numpy(), ref.ids), i
+        ok = ref.status == 0
+        assert np.array_equal(got["kept"].numpy()[ok], ref.kept[ok]), i
+        assert np.array_equal(got["thresh_id"].numpy()[ok], ref.thresh_id[ok]), i
+        assert np.array_equal(got["thresh_value"].numpy()[ok].view(np.uint32),
+                              ref.thresh_value[ok].view(np.uint32)), i
+        assert np.abs(got["logprob"].numpy()[ok] - ref.logprob[ok]).max() <= 1e-3, i
+
+
+@pytest.mark.gpu
+def test_raw_abi_logprob_and_decode_update():
+    """gtp_logprob_entropy_rows and gtp_decode_update_rows through ctypes on
+    caller-owned buffers: logprob / entropy against the oracle within 1e-3,
+    the decode bookkeeping against its definition."""
+    from graspo_amd import workloads as W
+    from tests import _capi
+    from tests._util import oracle_logprob
+
+    L = _capi.lib()
+    dev = torch.device("cuda:0")
+    for N, kind in ((300, "int32"), (77, "int64")):
+        x, t = W.logprob_workload(5, rows=N)
+        t = t.to(torch.int64) if kind == "int64" else t
+        xd, td = x.to(dev), t.to(dev)
+        lp = torch.empty(N, dtype=torch.float32, device=dev)
+        H = torch.empty(N, dtype=torch.float32, device=dev)
+        st = torch.full((N,), -7, dtype=torch.int32, device=dev)
+        print("raw abi logprob", N, kind, flush=True)
+        rc = L.gtp_logprob_entropy_rows(xd.data_ptr(), 1, N, x.shape[1], x.shape[1],
+                                        td.data_ptr(), int(kind == "int64"), lp.data_ptr(),
+                                        H.data_ptr(), st.data_ptr(), _capi.stream_handle())
+        assert rc == 0
+        torch.cuda.synchronize()
+        rlp, rH, rst = oracle_logprob(x, t)
+        assert (st.cpu().numpy() == 0).all()
+        assert np.abs(lp.cpu().numpy() - rlp).max() <= 1e-3
+        assert np.abs(H.cpu().numpy() - rH).max() <= 1e-3
+
+    B, pad, eos, col = 37, 0, 5, 3
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 9, (B,), generator=g)
+    status = (torch.rand(B, generator=g) < 0.1).to(torch.int32)
+    ids[status.bool()] = -1
+    fin = torch.rand(B, generator=g) < 0.2
+    want_ids = torch.where(status.bool(), torch.full_like(ids, pad), ids)
+    want_fin = fin | want_ids.eq(eos)
+    ids_d, st_d, fin_d = ids.to(dev), status.to(dev), fin.to(torch.uint8).to(dev)
+    seq = torch.full((B, 8), -3, dtype=torch.int64, device=dev)
+    attn = torch.zeros((B, 8), dtype=torch.uint8, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    print("raw abi decode update", flush=True)
+    rc = L.gtp_decode_update_rows(ids_d.data_ptr(), st_d.data_ptr(), B, eos, pad,
+                                  fin_d.data_ptr(), seq.data_ptr(), 8, attn.data_ptr(), 8, col,
+                                  flags.data_ptr(), _capi.stream_handle())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(ids_d.cpu(), want_ids)
+    assert torch.equal(fin_d.cpu().bool(), want_fin)
+    assert torch.equal(seq[:, col].cpu(), want_ids)
+    assert torch.equal(attn[:, col].cpu().bool(), want_ids.ne(pad))
+    assert flags.cpu().tolist() == [int((~want_fin).sum()), int(status.ne(0).sum())]

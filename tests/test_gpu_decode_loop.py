@@ -32,6 +32,8 @@ class ToyLM:
         self.masks = []
 
     def _logits(self, ids, start):
+        # an embedding lookup faults on an id outside [0, V): refuse it here
+        assert bool(((ids >= 0) & (ids < V)).all()), f"id outside [0, {V}) fed to the model"
         L = ids.shape[1]
         pos = torch.arange(start, start + L, device=DEV)
         out = self.table[(ids * 31 + pos[None, :] * 7) % 97].clone()  # [B, L, V] bf16
@@ -246,12 +248,15 @@ def test_update_kernel_against_torch(B):
     seq = torch.full((B, 9), -5, dtype=torch.int64, device=DEV)
     attn = torch.zeros((B, 9), dtype=torch.bool, device=DEV)
     flags = torch.full((2,), -1, dtype=torch.int32, device=DEV)
-    want_fin = fin | ids.eq(EOS)
+    ids[status.ne(0)] = -1  # the sampler's id for a bad row
+    want_ids = torch.where(status.ne(0), torch.full_like(ids, 3), ids)  # padded in place
+    want_fin = fin | want_ids.eq(EOS)
     fin_in = fin.clone()
     ops.decode_update(ids, status, fin_in, EOS, 3, seq, attn, 4, flags)
     torch.cuda.synchronize()
+    assert torch.equal(ids, want_ids)
     assert torch.equal(fin_in, want_fin)
-    assert torch.equal(seq[:, 4], ids) and bool((seq[:, :4] == -5).all())
+    assert torch.equal(seq[:, 4], want_ids) and bool((seq[:, :4] == -5).all())
     assert bool((seq[:, 5:] == -5).all())
-    assert torch.equal(attn[:, 4], ids.ne(3)) and not bool(attn[:, :4].any())
+    assert torch.equal(attn[:, 4], want_ids.ne(3)) and not bool(attn[:, :4].any())
     assert flags.tolist() == [int((~want_fin).sum()), int(status.ne(0).sum())]

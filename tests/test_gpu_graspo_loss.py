@@ -77,3 +77,53 @@ def test_three_dim_input_and_broadcast_advantages():
     got = GRASPOLoss(0.2)(a, old, adv, mask)  # advantages broadcast inside
     want = reference_loss(lp, old, adv, mask, 0.2)
     assert abs(float(got) - float(want)) <= 1e-6
+
+
+def _compare_elementwise(lp, old, adv, mask, eps):
+    """Loss and per-token gradient equal to torch's, NaN where torch has NaN."""
+    a = lp.clone().requires_grad_(True)
+    got = GRASPOLoss(eps)(a, old, adv, mask)
+    got.backward()
+    b = lp.clone().requires_grad_(True)
+    want = reference_loss(b, old, adv, mask, eps)
+    want.backward()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.detach(), want.detach(), rtol=1e-6, atol=1e-7, equal_nan=True)
+    assert torch.equal(a.grad.isnan(), b.grad.isnan()), (a.grad, b.grad)
+    torch.testing.assert_close(a.grad, b.grad, rtol=1e-6, atol=1e-9, equal_nan=True)
+
+
+def test_non_finite_logprobs_propagate_like_torch():
+    """NaN and +-inf log-probs, at masked and unmasked positions: torch's min
+    and clamp pass NaN through, NaN * 0 under the mask still poisons the
+    sum, and autograd puts NaN on the same gradient positions."""
+    B, T = 4, 16
+    g = torch.Generator().manual_seed(11)
+    lp = (-torch.rand(B, T, generator=g)).to(DEV)
+    old = (lp.cpu() + 0.2 * torch.randn(B, T, generator=g)).to(DEV)
+    adv = torch.randn(B, T, generator=g).to(DEV)
+    mask = torch.ones(B, T, dtype=torch.bool, device=DEV)
+    nan, inf = float("nan"), float("inf")
+    lp[0, 3] = nan                      # unmasked NaN
+    lp[1, 5] = nan                      # masked NaN
+    mask[1, 5] = False
+    lp[2, 7] = inf                      # r = inf with A > 0: s1 = inf
+    adv[2, 7] = 1.5
+    lp[2, 8] = -inf                     # r = 0
+    lp[3, 2] = inf                      # r = inf with A = 0: s1 = NaN, masked
+    adv[3, 2] = 0.0
+    mask[3, 2] = False
+    lp[3, 9] = inf                      # r = inf with A < 0: s1 = -inf
+    adv[3, 9] = -0.5
+    print("graspo loss non-finite: whole batch", flush=True)
+    _compare_elementwise(lp, old, adv, mask, 0.2)
+    # one sequence at a time, so a finite loss is compared where torch has one
+    for b in range(B):
+        print("graspo loss non-finite: sequence", b, flush=True)
+        _compare_elementwise(lp[b:b + 1].contiguous(), old[b:b + 1].contiguous(),
+                             adv[b:b + 1].contiguous(), mask[b:b + 1].contiguous(), 0.2)
+    # NaN in the advantages, and a float mask of zero weight on a NaN
+    adv2 = adv.clone()
+    adv2[0, 0] = nan
+    print("graspo loss non-finite: NaN advantage, float mask", flush=True)
+    _compare_elementwise(lp, old, adv2, mask.float(), 0.2)

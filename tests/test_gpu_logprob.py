@@ -122,3 +122,26 @@ def test_sequence_logprob_dropin_3d_views_and_grad():
     lg2 = logits.detach().clone().requires_grad_(True)
     torch.log_softmax(lg2, -1).gather(-1, ids.unsqueeze(-1)).sum().backward()
     assert float((lg.grad - lg2.grad).abs().max()) <= 1e-4
+
+
+def test_out_of_range_target_raises_like_gather():
+    """A target outside [0, V) raises RuntimeError, as the reference's
+    log_softmax(...).gather(...) (graspo_loss.py:19-21) and index_select
+    (tensor_utils.py:167-186) reject such an index, instead of a silent NaN."""
+    from graspo_amd.graspo_loss import sequence_log_probs_from_logits
+    from graspo_amd.tensor_utils import _selected_token_log_probs_from_hidden
+
+    dev = torch.device("cuda:0")
+    x = torch.randn(2, 5, 300, device=dev)
+    for bad in (300, -1):
+        t = torch.randint(0, 300, (2, 5), device=dev)
+        t[1, 3] = bad
+        print("out-of-range target", bad, flush=True)
+        with pytest.raises(RuntimeError, match="outside"):
+            sequence_log_probs_from_logits(x, t)
+        with pytest.raises(RuntimeError, match="outside"):
+            sequence_log_probs_from_logits(x.clone().requires_grad_(True), t)
+        h = torch.randn(2, 5, 64, device=dev)
+        w = torch.randn(300, 64, device=dev)
+        with pytest.raises(RuntimeError, match="outside"):
+            _selected_token_log_probs_from_hidden(h, w, t)

@@ -40,8 +40,15 @@ def assert_parity(g, ref, what=""):
     assert np.array_equal(g.thresh_value.numpy()[ok].view(np.uint32),
                           ref.thresh_value[ok].view(np.uint32)), what
     if ok.any():
-        assert np.abs(g.logprob.numpy()[ok] - ref.logprob[ok]).max() <= TOL, what
-        assert np.abs(g.sampled_logprob.numpy()[ok] - ref.sampled_logprob[ok]).max() <= TOL, what
+        # NaN where the oracle has NaN (greedy rows holding a NaN or +inf),
+        # -inf where it has -inf, within TOL elsewhere
+        for got, want in ((g.logprob.numpy()[ok], ref.logprob[ok]),
+                          (g.sampled_logprob.numpy()[ok], ref.sampled_logprob[ok])):
+            assert np.array_equal(np.isnan(got), np.isnan(want)), what
+            assert np.array_equal(np.isneginf(got), np.isneginf(want)), what
+            fin = np.isfinite(want)
+            if fin.any():
+                assert np.abs(got[fin] - want[fin]).max() <= TOL, what
 
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 5])
@@ -145,7 +152,11 @@ def test_rows_without_a_finite_value(dtype, params):
     x = x.to(dtype)
     kw = dict(params, uniforms=torch.full((6,), 0.25))
     g = gpu_sample(x, **kw)
-    assert g.status.tolist()[:4] == [1, 1, 2, 1], (dtype, params, g.status)
+    if params["temperature"] > 0:
+        assert g.status.tolist()[:4] == [1, 1, 2, 1], (dtype, params, g.status)
+    else:  # greedy is torch.argmax: NaN, then +inf, win; all -inf gives id 0
+        assert g.status.tolist() == [0] * 6, (dtype, g.status)
+        assert g.ids.tolist() == torch.argmax(x.float(), dim=-1).tolist()
     assert_parity(g, oracle_sample(x, **kw), f"{dtype} {params}")
 
 
@@ -210,3 +221,79 @@ def test_rejects_cpu_tensors_and_bad_args():
         ops.sample(xd, temperature=1.0, repetition_penalty=0.0, uniforms=torch.zeros(2).cuda())
     with pytest.raises(RuntimeError):
         ops.sample(torch.zeros(2, (1 << 18) + 8).cuda(), temperature=0.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [333, 4096, 151936])
+def test_greedy_non_finite_rows_match_torch_argmax(dtype, V):
+    """Greedy decoding is the reference's logits.argmax(dim=-1)
+    (tensor_utils.py:658): the first NaN wins, then the first +inf, ties and
+    all -inf rows go to the lowest id.  Checked against torch.argmax on the
+    same device rows and against the oracle, on the row-wise kernel (V 333)
+    and the split kernel (one and several slices per row)."""
+    g = torch.Generator().manual_seed(V)
+    B = 10
+    x = torch.randn(B, V, generator=g)
+    nan, inf = float("nan"), float("inf")
+    x[0, [V // 3, 7, V - 2]] = nan
+    x[1, [V // 2, 12]] = inf
+    x[2, V // 4] = inf
+    x[2, V - 30] = nan
+    x[3] = -inf
+    x[4] = -inf
+    x[4, [V // 3, 5]] = nan
+    x[5] = nan
+    x[6, 17] = -inf
+    x[7, [3, V - 1]] = 9.0
+    x[8, V // 2] = -inf
+    x[8, V // 2 + 1] = inf
+    x[9, V - 1] = nan
+    x = x.to(dtype)
+    print(f"greedy non-finite {dtype} V={V}", flush=True)
+    got = gpu_sample(x, temperature=0.0)
+    want = torch.argmax(x.to("cuda:0"), dim=-1).cpu()
+    assert got.status.tolist() == [0] * B, got.status
+    assert torch.equal(got.ids, want), (got.ids, want)
+    assert_parity(got, oracle_sample(x, temperature=0.0), "greedy non-finite")
+    # the drop-in returns the same ids without raising
+    from graspo_amd import tensor_utils as tu
+    ids = tu._next_token_from_logits(x.to("cuda:0"), temperature=0.0, top_p=1.0)
+    assert torch.equal(ids.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_non_finite_rows_under_mask_and_penalty(dtype):
+    """The argmax runs over allowed tokens with penalised values: a masked
+    NaN or +inf loses, a row whose allowed tokens are all -inf returns its
+    first allowed token, no allowed token is EMPTY, and a penalty can push a
+    finite value to +inf (x / rho, rho < 1).  Against the oracle, on both
+    kernels."""
+    for V in (333, 151936):
+        g = torch.Generator().manual_seed(V + 1)
+        B = 6
+        x = torch.randn(B, V, generator=g)
+        nan, inf = float("nan"), float("inf")
+        x[0, [40, 7]] = nan
+        x[1, [90, 12]] = inf
+        x[2] = -inf
+        x[3, 100] = 3.0e38
+        x[4, 200] = nan
+        bits = torch.rand(B, V, generator=g) < 0.3
+        bits[0, 40] = False
+        bits[0, 7] = True
+        bits[1, [90, 12]] = False
+        bits[2] = False
+        bits[2, [77, 210]] = True
+        bits[3, 100] = True
+        bits[5] = False
+        hist = torch.full((B, 4), -1, dtype=torch.int32)
+        hist[3, 0] = 100
+        hist[4, 0] = 200
+        x = x.to(dtype)
+        kw = dict(temperature=0.0, allow_mask=W.pack_mask(bits), history=hist,
+                  repetition_penalty=0.5)
+        print(f"greedy non-finite masked {dtype} V={V}", flush=True)
+        got = gpu_sample(x, **kw)
+        ref = oracle_sample(x, **kw)
+        assert ref.ids[0] == 7 and ref.ids[2] == 77 and ref.ids[3] == 100 and ref.status[5] == 2
+        assert_parity(got, ref, f"greedy masked V={V}")

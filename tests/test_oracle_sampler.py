@@ -107,6 +107,100 @@ def test_greedy_and_top1_are_argmax_first_index():
     assert np.allclose(k1.sampled_logprob, 0.0)
 
 
+def greedy_nonfinite_rows(V=333, seed=21):
+    """Rows where torch.argmax's NaN and inf rules decide the answer."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((10, V)).astype(np.float32)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    X[0, [40, 7, 200]] = nan                 # first NaN wins
+    X[1, [90, 12]] = inf                     # first +inf wins
+    X[2, 50] = inf
+    X[2, 260] = nan                          # NaN beats +inf
+    X[3] = -inf                              # all -inf: id 0
+    X[4] = -inf
+    X[4, [100, 5]] = nan
+    X[5, :] = nan                            # all NaN: id 0
+    X[6, 17] = -inf                          # finite row with a -inf
+    X[7, [3, 300]] = 9.0                     # plain tie
+    X[8, 150] = -inf
+    X[8, 151] = inf
+    X[9, V - 1] = nan                        # NaN at the last id
+    return X
+
+
+def test_greedy_non_finite_rows_are_torch_argmax():
+    """Greedy is logits.argmax(dim=-1) (tensor_utils.py:658): a NaN beats every
+    value, +inf every finite one, ties and all -inf rows go to the lowest id.
+    The oracle agrees with torch.argmax itself on every row, in fp32 and bf16,
+    status OK throughout, with a NaN logprob on rows holding a NaN or +inf."""
+    X = greedy_nonfinite_rows()
+    for dt, arr in ((O.DTYPE_F32, X),
+                    (O.DTYPE_BF16, torch.from_numpy(X).bfloat16().view(torch.int16).numpy()
+                     .view(np.uint16))):
+        r = O.sample_rows(arr, dt, temperature=0.0)
+        xt = torch.from_numpy(X)
+        want = torch.argmax(xt if dt == O.DTYPE_F32 else xt.bfloat16(), dim=-1).numpy()
+        assert (r.ids == want).all(), (r.ids, want)
+        assert (r.status == 0).all() and (r.kept == 1).all()
+        bad = np.isnan(X).any(1) | np.isposinf(X).any(1) | np.isneginf(X).all(1)
+        assert np.isnan(r.logprob[bad]).all() and np.isfinite(r.logprob[~bad]).all()
+    sem = O.sample_semantic(X, temperature=0.0)
+    assert [s[0] for s in sem] == r.ids.tolist()
+
+
+def test_greedy_non_finite_rows_under_mask_and_penalty():
+    """With an allow mask the argmax runs over allowed tokens only (a NaN or
+    +inf outside the mask loses); a row whose allowed tokens are all -inf
+    returns the first allowed token; no allowed token at all is EMPTY.  The
+    penalty maps NaN to NaN and +inf to +inf, and can push a finite value to
+    +inf (x / rho with rho < 1)."""
+    X = greedy_nonfinite_rows()
+    V = X.shape[1]
+    rng = np.random.default_rng(5)
+    allow = rng.random((10, V)) < 0.3
+    allow[0, 40] = False                      # mask the first NaN: NaN at 7 wins
+    allow[0, 7] = True
+    allow[1, [90, 12]] = False                # both +inf masked: finite argmax
+    allow[3, :] = False
+    allow[3, [77, 210]] = True                # all -inf: first allowed (77)
+    allow[5, :] = False                       # nothing allowed: EMPTY
+    words = np.zeros((10, (V + 31) // 32), np.uint32)
+    for b in range(10):
+        for i in np.flatnonzero(allow[b]):
+            words[b, i >> 5] |= np.uint32(1 << (i & 31))
+    X2 = X.copy()
+    X2[6, 100] = np.float32(3.0e38)           # penalised with rho 0.5: +inf
+    allow[6, 100] = True
+    words[6, 100 >> 5] |= np.uint32(1 << (100 & 31))
+    hist = np.full((10, 4), -1, np.int32)
+    hist[6, 0] = 100
+    hist[7, :2] = [3, 300]
+    r = O.sample_rows(X2, O.DTYPE_F32, temperature=0.0, allow_mask=words, history=hist,
+                      repetition_penalty=0.5)
+    sem = O.sample_semantic(X2, temperature=0.0, allow_mask=words, history=hist,
+                            repetition_penalty=0.5)
+    assert r.ids[0] == 7 and r.ids[3] == 77 and r.ids[6] == 100
+    assert r.status[5] == O.ROW_EMPTY and r.ids[5] == -1
+    ok = r.status == 0
+    assert ok.sum() == 9
+    assert [s[0] for s in sem] == r.ids.tolist()
+    # brute force over the contract, row by row
+    for b in range(10):
+        cand = [i for i in range(V) if allow[b, i]]
+        if not cand:
+            continue
+        ys = []
+        for i in cand:
+            x = X2[b, i]
+            y = x
+            if i in set(hist[b][hist[b] >= 0].tolist()):
+                y = np.float32(x * np.float32(0.5)) if x < 0 else np.float32(x / np.float32(0.5))
+            ys.append(np.float32(y + np.float32(0.0)))
+        nans = [i for i, y in zip(cand, ys) if np.isnan(y)]
+        best = nans[0] if nans else cand[int(np.argmax(np.array(ys)))]
+        assert r.ids[b] == best, (b, r.ids[b], best)
+
+
 def test_top_k_set_matches_torch_topk():
     rng = np.random.default_rng(4)
     X = (rng.standard_normal((8, 5000)) * 3).astype(np.float32)  # no exact ties
