@@ -1424,6 +1424,65 @@ extern "C" int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t
                           out_thresh_id, out_status, workspace, workspace_bytes, false, stream);
 }
 
+// ------------------------------------------------ the entry point without allocation
+//
+// gtp_sample_rows_noalloc runs gtp_sample_rows with the library's own
+// workspace: a file-scope device array of GTP_NOALLOC_SCRATCH_BYTES, one copy
+// per GPU for the life of the process.  Host code never passes the array's
+// name to a kernel (on the host it is a stand-in, not a device address): the
+// first call on each device, with that device current, looks up that
+// device's copy with hipGetSymbolAddress and keeps the address in a
+// per-device table, and every launch takes the address from the table.
+static __device__ __align__(256) unsigned char scratch[GTP_NOALLOC_SCRATCH_BYTES];
+
+namespace gtp {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's copy of `scratch`, or nullptr when it cannot be found.
+void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace gtp
+
+extern "C" int gtp_sample_rows_noalloc(const void* logits, int dtype, int64_t B, int64_t V,
+                                       int64_t row_stride, const int32_t* history,
+                                       int64_t hist_len, int64_t hist_stride,
+                                       const uint32_t* allow_mask, int64_t mask_stride,
+                                       const float* uniforms, const gtp_sampler_params* params,
+                                       const uint8_t* finished, int64_t pad_token_id,
+                                       int64_t* out_ids, float* out_logprob,
+                                       float* out_sampled_logprob, int32_t* out_kept,
+                                       float* out_thresh_value, int32_t* out_thresh_id,
+                                       int32_t* out_status, void* stream) {
+  if (!params || B < 0 || V <= 0) return GTP_ERR_INVALID_ARGUMENT;
+  if (B == 0) return GTP_OK;
+  const size_t need = gtp_sample_workspace_bytes(dtype, B, V, params);
+  if (need > GTP_NOALLOC_SCRATCH_BYTES) return GTP_ERR_UNSUPPORTED;
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_for_current_device();
+    if (!ws) return GTP_ERR_LAUNCH;
+  }
+  return sample_rows_impl(logits, dtype, B, V, row_stride, history, hist_len, hist_stride,
+                          allow_mask, mask_stride, uniforms, params, finished, pad_token_id,
+                          out_ids, out_logprob, out_sampled_logprob, out_kept, out_thresh_value,
+                          out_thresh_id, out_status, ws, GTP_NOALLOC_SCRATCH_BYTES, true, stream);
+}
+
 namespace gtp {
 
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {

@@ -15,8 +15,9 @@
  *   - All array pointers are DEVICE pointers owned by the caller.  The library
  *     never allocates and is reentrant.  Its only mutable global state is:
  *     the measurement hook's per-thread event pair (gtp_time_next_launch);
- *     and a per-device cache of the compute-unit count, filled once per
- *     device with atomic stores.
+ *     a per-device cache of the compute-unit count, filled once per device
+ *     with atomic stores; and the per-device scratch array of
+ *     gtp_sample_rows_noalloc with its per-device address table.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL is the default stream).
  *   - Return value: GTP_OK or a GTP_ERR_* code for a bad argument or a failed
@@ -150,6 +151,36 @@ int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
  */
 size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                   const gtp_sampler_params* params);
+
+/* Size of the library's own workspace for gtp_sample_rows_noalloc. */
+#define GTP_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+/*
+ * gtp_sample_rows_noalloc -- gtp_sample_rows without a caller workspace and
+ * without any allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments and results are those of gtp_sample_rows (same kernels, same
+ * bit-exact outputs).  The workspace is a device array of
+ * GTP_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends; the first call on a device looks up that device's copy.
+ * Each call first clears the array's per-row counters with a small fill
+ * kernel on `stream`.  Returns GTP_ERR_UNSUPPORTED when the call needs more
+ * than GTP_NOALLOC_SCRATCH_BYTES (gtp_sample_workspace_bytes() tells), e.g.
+ * thousands of fp32 rows of a 2^18 vocabulary.  Every call on one GPU shares
+ * that GPU's array: calls that may overlap on one GPU (different streams,
+ * host threads) race and must be serialised by the caller.
+ */
+int gtp_sample_rows_noalloc(const void* logits, int dtype, int64_t B, int64_t V,
+                            int64_t row_stride, const int32_t* history, int64_t hist_len,
+                            int64_t hist_stride, const uint32_t* allow_mask,
+                            int64_t mask_stride, const float* uniforms,
+                            const gtp_sampler_params* params, const uint8_t* finished,
+                            int64_t pad_token_id, int64_t* out_ids, float* out_logprob,
+                            float* out_sampled_logprob, int32_t* out_kept,
+                            float* out_thresh_value, int32_t* out_thresh_id,
+                            int32_t* out_status, void* stream);
 
 /*
  * gtp_logprob_entropy_rows -- log_softmax(x)[target] and softmax entropy per

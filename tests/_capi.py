@@ -27,6 +27,8 @@ def lib() -> ctypes.CDLL:
     L = ctypes.CDLL(graspo_amd.LIB_PATH)
     L.gtp_sample_rows.argtypes = _SAMPLE_ARGS + [VP, SZ, VP]
     L.gtp_sample_rows.restype = I32
+    L.gtp_sample_rows_noalloc.argtypes = _SAMPLE_ARGS + [VP]
+    L.gtp_sample_rows_noalloc.restype = I32
     L.gtp_sample_workspace_bytes.argtypes = [I32, I64, I64, ctypes.POINTER(SamplerParams)]
     L.gtp_sample_workspace_bytes.restype = SZ
     L.gtp_logprob_entropy_rows.argtypes = [VP, I32, I64, I64, I64, VP, I32, VP, VP, VP, VP]
@@ -70,7 +72,7 @@ class SampleBuffers:
 
 def sample_args(logits: torch.Tensor, *, temperature, top_k=0, top_p=1.0,
                 repetition_penalty=1.0, history=None, allow_mask=None, uniforms=None):
-    """Leading arguments of gtp_sample_rows for [B, V] logits with
+    """Leading arguments of gtp_sample_rows / _noalloc for [B, V] logits with
     contiguous rows; returns (args, params, B)."""
     B, V = logits.shape
     p = SamplerParams(float(temperature), int(top_k), float(top_p), float(repetition_penalty))
