@@ -387,7 +387,8 @@ __device__ RadixResult radix_search(SamplerSmem& sm, const Row<T>& r, float m, b
 // ---------------------------------------------------------------- kernel
 
 // One row (block-uniform; every thread of the 1024-thread workgroup calls it).
-template <typename T>
+// NG: groups per thread per stream step (fewer registers for a smaller NG)
+template <typename T, int NG = kSG>
 __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, SamplerSmem& sm) {
   const int tid = threadIdx.x;
 
@@ -423,12 +424,12 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   // ---- 1. stream pass
   LseState ls{kNegInf, 0.0f};
   float tl = kNegInf;
-  constexpr int64_t kStep = (int64_t)kSB * kSG;
+  constexpr int64_t kStep = (int64_t)kSB * NG;
   for (int64_t base = 0; base < r.ngroups; base += kStep) {
-    float x[kSG][8];
-    uint32_t mb[kSG], pb[kSG];
+    float x[NG][8];
+    uint32_t mb[NG], pb[NG];
 #pragma unroll
-    for (int k = 0; k < kSG; ++k) {
+    for (int k = 0; k < NG; ++k) {
       const int64_t G = base + k * kSB + tid;
       if (G < r.ngroups) {
         load_group<T>(r.x, G, r.V, r.vec_ok, x[k]);
@@ -443,7 +444,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     }
     float cm = kNegInf;
 #pragma unroll
-    for (int k = 0; k < kSG; ++k) {
+    for (int k = 0; k < NG; ++k) {
       const int64_t G = base + k * kSB + tid;
       float ghi;
       if (a.mask) {
@@ -461,7 +462,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
       if (G < r.ngroups) sm.u.gkey[G] = (uint16_t)ord16(bf16_round_up(ghi));
       if ((mb[k] & pb[k]) == 0u) tl = fmaxf(tl, ghi);
     }
-    lse_fold<kSG>(ls, x, cm);
+    lse_fold<NG>(ls, x, cm);
   }
   const LseState row_lse = block_lse(sm, ls);
   // logprob = x - m - ln s, rounded once (raw_logprob)
@@ -536,7 +537,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     // ---- 3. re-read passing groups, exact candidates
     for (int64_t base = 0; base < r.ngroups; base += kStep) {
 #pragma unroll
-      for (int k = 0; k < kSG; ++k) {
+      for (int k = 0; k < NG; ++k) {
         const int64_t G = base + k * kSB + tid;
         if (G < r.ngroups && (uint32_t)sm.u.gkey[G] >= gk_thr) {
           float x[8];
@@ -1924,13 +1925,41 @@ __global__ __launch_bounds__(kSB) void sampler_hist_kernel(SamplerArgs a) {
 
 }  // namespace gtp
 
+#include "tokpath_sampler_topp.h"
+
 using namespace gtp;
 
 namespace gtp {
 
+// The rows sampler_topp_kernel handed over (handover[0] of them, indices in
+// handover[1..]), on the row-wise path, one after another in one workgroup;
+// then the count and the list return to zero, so the workspace is all zero
+// again for the next call (the split kernel's arrival counters share it).
+// With no row handed over it reads one word and exits.
+__global__ __launch_bounds__(kSB) void sampler_handover_kernel(SamplerArgs a,
+                                                               uint32_t* __restrict__ handover) {
+  __shared__ SamplerSmem sm;
+  const uint32_t n = handover[0];
+  if (n == 0u) return;
+  for (uint32_t i = 0; i < n; ++i) {
+    rowwise_row<uint16_t>(a, (int64_t)handover[1 + i], sm);
+    __syncthreads();
+  }
+  for (uint32_t i = threadIdx.x; i <= n; i += kSB) handover[i] = 0u;
+}
+
+size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p) {
+  const bool top_p = p->top_p > 0.0f && p->top_p < 1.0f && (p->top_k <= 0 || (int64_t)p->top_k >= V);
+  if (dtype != GTP_DTYPE_BF16 || !(p->temperature > 0.0f) || !(p->temperature <= 1024.0f) ||
+      !top_p || V < topp::kMinV || V > GTP_SAMPLER_MAX_V || B <= 0)
+    return 0;
+  return ((size_t)(B + 1) * 4 + 255) / 256 * 256;
+}
+
 // One workgroup of 1024 threads per row; handles every row layout, vocabulary
 // and parameter combination the contract allows.
-int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s) {
+int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
+                           void* workspace, size_t workspace_bytes) {
   const dim3 grid((unsigned)B), block(kSB);
   // bf16 sampling rows on 16-byte aligned rows take the value-histogram
   // kernel (temperature bounded so that distinct bf16 values keep distinct,
@@ -1938,6 +1967,20 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   const bool aligned = (reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0 &&
                        ((a.row_stride * 2) & 15) == 0;
   // (penalised counts are 16-bit: at most 65535 history entries)
+  // top-p rows without top-k: the single-read top-p kernel, then the
+  // row-wise path for any row it hands over (the hand-over list lives in the
+  // workspace; without one, the value-histogram kernel below takes the call)
+  gtp_sampler_params p{a.T, a.K, a.P, a.rho};
+  const size_t tw = topp_workspace_bytes(dtype, B, a.V, &p);
+  if (tw > 0 && aligned && a.hist_len <= 65535 && workspace && workspace_bytes >= tw) {
+    uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
+    if (a.mask)
+      launch_timed(sampler_topp_kernel<true>, grid, block, s, a, handover);
+    else
+      launch_timed(sampler_topp_kernel<false>, grid, block, s, a, handover);
+    hipLaunchKernelGGL(sampler_handover_kernel, dim3(1), block, 0, s, a, handover);
+    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+  }
   if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&
       a.hist_len <= 65535) {
     if (a.mask)

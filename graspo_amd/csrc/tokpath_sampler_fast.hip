@@ -1391,7 +1391,7 @@ extern "C" size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                              const gtp_sampler_params* params) {
   if (!params || B <= 0 || V <= 0) return 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, true);
-  return pl.fast ? pl.ws_bytes : 0;
+  return pl.fast ? pl.ws_bytes : topp_workspace_bytes(dtype, B, V, params);
 }
 
 namespace gtp {
@@ -1539,7 +1539,13 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
   const bool aligned = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 &&
                        ((row_stride * es) & 15) == 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, aligned);
-  if (!pl.fast) return launch_sampler_general(a, dtype, B, st);
+  if (!pl.fast) {
+    const size_t tw = topp_workspace_bytes(dtype, B, V, params);
+    if (clear_counters && tw > 0 && workspace && workspace_bytes >= tw)
+      hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, st,
+                         reinterpret_cast<uint32_t*>(workspace), (int64_t)1);
+    return launch_sampler_general(a, dtype, B, st, workspace, workspace_bytes);
+  }
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes))
     return GTP_ERR_INVALID_ARGUMENT;
   if (clear_counters && pl.ws_bytes > 0) {

@@ -33,7 +33,14 @@ struct SamplerArgs {
 };
 
 // One workgroup of 1024 threads per row (any layout, V <= GTP_SAMPLER_MAX_V).
-int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s);
+// Top-p bf16 rows use `workspace` (topp_workspace_bytes of it, zeroed once)
+// for the rows the top-p kernel hands over to the row-wise path.
+int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
+                           void* workspace, size_t workspace_bytes);
+
+// Workspace of the top-p path for these parameters (0 when another path
+// takes the call): the hand-over count and list of rows.
+size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p);
 
 // Greedy decoding (T <= 0) is the reference's logits.argmax(dim=-1)
 // (src/graspo/backends/graspoflow/tensor_utils.py:658) over the allowed
@@ -49,7 +56,7 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
 // penalised ids.  Lane 0 writes the row's outputs; logprob is NaN when the
 // raw row holds a NaN or +inf (`raw_nonfinite`), as log_softmax gives.
 template <typename T>
-__device__ __noinline__ void greedy_argmax_rescan(const SamplerArgs& a, int64_t b, uint32_t* pen,
+__device__ __forceinline__ void greedy_argmax_rescan(const SamplerArgs& a, int64_t b, uint32_t* pen,
                                                   bool rebuild_pen, bool raw_nonfinite,
                                                   float lse_m, float lse_ln) {
   const int lane = threadIdx.x & (kWave - 1);
