@@ -1974,10 +1974,13 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   const size_t tw = topp_workspace_bytes(dtype, B, a.V, &p);
   if (tw > 0 && aligned && a.hist_len <= 65535 && workspace && workspace_bytes >= tw) {
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
-    if (a.mask)
-      launch_timed(sampler_topp_kernel<true>, grid, block, s, a, handover);
-    else
-      launch_timed(sampler_topp_kernel<false>, grid, block, s, a, handover);
+    const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
+    switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
+      case 0: launch_timed(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
+      case 1: launch_timed(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
+      case 2: launch_timed(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
+      default: launch_timed(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
+    }
     hipLaunchKernelGGL(sampler_handover_kernel, dim3(1), block, 0, s, a, handover);
     return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
   }

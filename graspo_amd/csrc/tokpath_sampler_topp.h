@@ -8,122 +8,193 @@
 // threads per row reads the row once; the answer follows the contract of
 // include/graspo_tokpath.h bit for bit.
 //
-// 1. Pilot.  Stream chunks are handed out in an order that starts the 16
-//    waves at 16 evenly spaced places of the row.  Their first chunks (16384
-//    tokens) are a sample: a two-pass radix select over the allowed tokens'
-//    16-bit order keys picks theta, a value with about 4096 allowed tokens of
-//    the row at or above it.
-// 2. Stream.  Per allowed token one LDS add into a 16-bit count per bf16
-//    value: unpenalised and penalised tokens (history ids, an LDS bitmap) in
-//    two histograms of 16384 values (exponents [87, 151) of both signs),
-//    zeros in two counters.  Allowed tokens whose processed value before
-//    temperature (x, or pen(x) for a history id) reaches theta go with their
-//    id into an LDS pool.  The raw log-sum-exp is folded for the logprob.
-// 3. Totals.  m = the largest processed logit y.  Thread t owns 16 value
-//    bins (thread 0 the largest values) and the penalised values whose y
-//    lies between its bins; its weight total (DETEXP_FIX(y - m) per distinct
-//    value times the count) and count total go through one block scan in
-//    descending order.
-// 4. Cut and draw.  The thread whose range holds floor(P W) (then
-//    floor(u W')) is resolved by one wave: its at most 64 distinct values
-//    sorted by y, a wave scan, and an integer quotient inside the tied
-//    values (all tokens of one value share one weight).
-// 5. Ids.  The k-th token of the cut value and the j-th of the drawn value,
-//    in id order: from the pool (the matching entries set bits of an id
-//    bitmap; a scan of popcounts finds the k-th), or, for a value below
-//    theta, from a rescan of the row.
-// Outside these bounds -- a value outside the bins, a count that overflows
-// 16 bits, more than 46 penalised values in one resolved range, a processed
-// logit outside the bins' range -- the row is handed over to the row-wise
-// path, which runs in a second launch (a block-uniform decision, taken
-// before any output of the row is written).
+// Value bins.  A bf16 value with biased exponent in [87, 150) has a 13-bit
+// magnitude index i; word i of a region holds two 16-bit counts, the
+// positive value in the low half and the negative one in the high half.
+// Per token the stream computes the byte offset of its word with packed
+// 16-bit arithmetic on the token pair a 32-bit load returns (and, sub,
+// min, shift: two tokens per instruction) and adds 1 or 0x10000 to it in
+// LDS: about six instructions per token, no branch.  Zeros, values outside
+// the exponent range, infinities and NaN fall into an escape word; a row
+// with any escape is handed over.  Region A counts the allowed unpenalised
+// tokens; region 2 counts the allowed penalised tokens (by raw value) or,
+// with a mask and no penalty, the masked tokens (for the raw log-sum-exp).
+// With both a mask and a penalty, masked tokens go to per-lane spill words
+// and the raw log-sum-exp is folded per token.
+//
+// 1. Pilot.  The first chunk of each wave (16 evenly spaced places of the
+//    row) is counted; one block scan over the counts picks theta, the value
+//    with about 1200 sampled-to-scale allowed tokens at or above it.
+// 2. Stream.  Counts per token; a vector (8 tokens) with an allowed token at
+//    or above theta goes whole into an LDS pool (16 bytes and its index).
+// 3. Totals.  Thread t owns the value bins 16t..16t+15 (descending values)
+//    and the penalised values whose processed logit y lies between them;
+//    its weight total (DETEXP_FIX(y - m) per value times the count) and
+//    count go through one block scan in descending order.  The raw
+//    log-sum-exp comes from the same counts.
+// 4. Cut and draw.  One wave finds the thread whose range holds floor(P W)
+//    (then floor(u W')) from the stored prefixes, ranks the range's values
+//    by y and takes the position inside the tied value (all its tokens
+//    share one weight) as an integer quotient.
+// 5. Ids.  The k-th token (id order) of the cut value and the j-th of the
+//    drawn value come from the pool when every token of both values is in
+//    it; otherwise from one more read of the row.
+// Outside these bounds (an escape, a 16-bit count overflow, a penalised
+// value above every bin, more than 48 penalised values in one resolved
+// range) the row is handed over to the row-wise path, which runs in a
+// second launch; the decision is block-uniform and taken before any output
+// of the row is written.
 #pragma once
 
 namespace gtp {
 namespace topp {
 
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef short ss2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ us2 as_us2(uint32_t w) { return __builtin_bit_cast(us2, w); }
+__device__ __forceinline__ ss2 as_ss2(uint32_t w) { return __builtin_bit_cast(ss2, w); }
+__device__ __forceinline__ uint32_t as_u32(us2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ uint32_t as_u32(ss2 v) { return __builtin_bit_cast(uint32_t, v); }
+
 constexpr int kB = 1024;             // threads per row
 constexpr int kW = kB / kWave;       // waves per row
-constexpr int kG = 2;                // vectors per lane per chunk
-constexpr int kChunk = kWave * kG;   // vectors per chunk
-constexpr int kBins = 16384;         // bf16 values with biased exponent in [87, 151), both signs
-constexpr uint32_t kELo = 87;
-constexpr int kPer = kBins / kB;     // bins per thread
-constexpr int kPool = 8192;          // captured tokens
-constexpr uint32_t kTarget = 4096;   // tokens the pilot aims to capture
-constexpr int kPenLanes = 46;        // penalised values one resolved range may hold
+constexpr int kG = 4;                // vectors per lane per chunk
+constexpr int kChunk = kWave * kG;   // vectors per chunk (2048 tokens, 64 mask words)
+constexpr uint32_t kELo = 87;        // smallest binned biased exponent
+constexpr uint32_t kBase = kELo << 7;
+constexpr uint32_t kNI = 63u * 128u;  // magnitude indices per sign (index 0: zero and tiny values)
+constexpr int kNV = 2 * (int)kNI;     // value bins, index 0 = the largest value
+constexpr int kPer = 16;              // value bins per owning thread
+constexpr int kOwners = kNV / kPer;   // threads that own value bins
+constexpr uint32_t kR2 = 8192;        // first word of region 2 (byte offset 32768)
+constexpr uint32_t kJunk = 8160;      // word for vectors past the row's end
+constexpr uint32_t kSpill = 16320;    // 64 per-lane spill words (mask and penalty)
+constexpr int kHistWords = 16384;
+constexpr int kPoolV = 3584;          // captured vectors (without a penalty)
+constexpr int kPoolVPen = 1536;       // ... with one (the penalty bitmap takes the rest)
+constexpr uint32_t kTarget = 2560;    // tokens the pilot aims to capture (without a penalty)
+constexpr uint32_t kTargetPen = 1100;
+constexpr int kPenLanes = 48;         // penalised values one resolved range may hold
+constexpr int kSmall = 64;            // values with at most this many tokens rank from a list
+constexpr int kRescanBuf = 512;       // ids one wave keeps per value in a rescan
+constexpr int kRescanG = 4;           // vectors per lane per rescan step
 constexpr int64_t kMinV = 65536;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
 
 struct Level {
-  float y;              // processed logit of the value
-  int32_t ubin;         // unpenalised bin of the value, or -1
-  int32_t pbin;         // penalised raw bin whose y ties, or -1
-  int32_t zero_u;       // 1: the unpenalised zeros belong to the level
-  int32_t zero_p;       // 1: the penalised zeros belong to the level
-  uint32_t n;           // tokens of the level
-  uint32_t k;           // position of the wanted token in id order
-  uint32_t n_before;    // tokens before the level
-  unsigned long long s_before;  // weight before the level
-  unsigned long long w;         // weight of one token of the level
+  float y;                      // processed logit of the value
+  uint32_t hu;                  // bf16 bits of its unpenalised tokens, kNone: none
+  uint32_t hp;                  // bf16 bits of its penalised tokens, kNone: none
+  uint32_t n;                   // tokens of the value
+  uint32_t k;                   // position of the wanted token in id order
+  uint32_t n_before;            // tokens before the value
+  unsigned long long s_before;  // weight before the value
+  unsigned long long w;         // weight of one of its tokens
 };
 
 struct alignas(16) Smem {
-  uint32_t cnt[kBins / 2];                // allowed unpenalised tokens per value (16-bit halves)
-  uint32_t pcnt[kBins / 2];               // allowed penalised tokens per raw value
-  uint32_t pen[GTP_SAMPLER_MAX_V / 32];   // penalised ids
-  uint32_t qid[kPool];                    // pool: id, bit 31 set for a penalised token
-  uint16_t qh[kPool];                     // pool: bf16 pattern
-  uint32_t sel[2][256];                   // pilot radix histograms
-  float red_f[kW][3];
-  uint32_t red_u[kW][2];
+  // counts (regions A and 2, junk and spill words); after the cut and the
+  // draw: id lists, id bitmaps or rescan buffers
+  uint32_t hist[kHistWords];
+  // pool: captured vectors; with a penalty, entries [kPoolVPen, kPoolV)
+  // hold the bitmap of penalised ids (GTP_SAMPLER_MAX_V bits)
+  u32x4 qd[kPoolV];
+  uint16_t qv[kPoolV];  // ... their vector index
+  union {
+    struct {
+      unsigned long long w[kB];  // penalised values' weight per owning thread
+      uint32_t c[kB];            // ... and count
+    } own;
+    struct {
+      unsigned long long w[kB + 1];  // weight before each thread's range (then the total)
+      uint32_t c[kB + 1];            // count before each thread's range
+    } ex;
+  } x;
   unsigned long long red_w[kW];
-  Level lv[2];                            // the cut (0) and the drawn (1) value
+  uint32_t red_u[kW][4];
+  float red_f[kW][3];
+  Level lv[2];  // the cut (0) and the drawn (1) value
   int32_t id_out[2];
-  uint32_t scan_n[kW][2];                 // rescan: matches per wave
-  uint32_t chunk_ctr;
+  uint32_t scan_n[kW][2];
   uint32_t pool_n;
-  uint32_t drop_key;     // largest ord32 key of a capture that found the pool full, 0: none
-  uint32_t theta_sel[2];
-  uint32_t n_counted;    // allowed tokens added to the two histograms
-  uint32_t zc, pz;       // allowed unpenalised / penalised zeros
-  unsigned long long o_ew[2];  // the resolved ranges: weight and count before them,
-  uint32_t o_ec[2];            // their penalised raw bins [o_pl, o_ph]
-  int32_t o_pl[2], o_ph[2];
-  uint32_t flags;        // bit 0: allowed value outside the bins; bit 1: bad history id
-  int32_t owner[2];
-  int32_t bad;           // fallback decided by a single wave
+  uint32_t list_n[2];
+  uint32_t chunk_ctr;
+  uint32_t drop_ord;  // largest ord16 key of a vector the full pool dropped, 0: none
+  uint32_t theta;     // bf16 bits of theta, kNone: every allowed token is captured
+  uint32_t flags;     // bit 0: hand over; bit 1: bad history id
+  int32_t bad;
+  __device__ __forceinline__ uint32_t* pen() { return reinterpret_cast<uint32_t*>(&qd[kPoolVPen]); }
+  __device__ __forceinline__ const uint32_t* pen() const {
+    return reinterpret_cast<const uint32_t*>(&qd[kPoolVPen]);
+  }
 };
 
-__device__ __forceinline__ int bin_of(uint32_t h) {  // -1 outside the bins
-  const uint32_t idx = (h & 0x7FFFu) - (kELo << 7);
-  if (idx >= 64u * 128u) return -1;
-  return (h & 0x8000u) ? (int)(kBins / 2 - 1 - idx) : (int)(kBins / 2 + idx);
+// Magnitude index i of a bf16 value: 0 for zeros and values below 2^-40
+// (the zero bin), mag - (kBase - 1) for the exponents [87, 150) (the last
+// magnitude aside), kNI (the escape word) above.
+// Value bin v (0 = the largest) <-> word, half and bf16 bits; the two zero
+// bins (v = kNI - 1 and kNI) stand for the value 0.
+constexpr int kZeroPos = (int)kNI - 1, kZeroNeg = (int)kNI;
+__device__ __forceinline__ uint32_t vb_word(int v) {
+  return v < (int)kNI ? kNI - 1u - (uint32_t)v : (uint32_t)v - kNI;
 }
-__device__ __forceinline__ uint32_t bin_bits(int b) {
-  return b >= kBins / 2 ? (uint32_t)(b - kBins / 2) + (kELo << 7)
-                        : 0x8000u | ((uint32_t)(kBins / 2 - 1 - b) + (kELo << 7));
+__device__ __forceinline__ uint32_t vb_shift(int v) { return v < (int)kNI ? 0u : 16u; }
+__device__ __forceinline__ uint32_t vb_bits(int v) {  // (the zero bins: 0x0000 / 0x8000)
+  const uint32_t i = vb_word(v);
+  const uint32_t mag = i ? i + kBase - 1u : 0u;
+  return v < (int)kNI ? mag : 0x8000u | mag;
 }
-__device__ __forceinline__ float bin_x(int b) { return u2f(bin_bits(b) << 16); }
-__device__ __forceinline__ uint32_t count16(const uint32_t* c, int b) {
-  return (c[b >> 1] >> ((b & 1) * 16)) & 0xFFFFu;
+__device__ __forceinline__ float vb_x(int v) { return vb_word(v) ? u2f(vb_bits(v) << 16) : 0.0f; }
+__device__ __forceinline__ int vb_of(uint32_t h) {  // -1 outside the bins
+  const uint32_t mag = h & 0x7FFFu;
+  const uint32_t i = mag < kBase ? 0u : mag - (kBase - 1u);
+  if (i >= kNI) return -1;
+  return (h & 0x8000u) ? (int)(kNI + i) : (int)(kNI - 1u - i);
+}
+__device__ __forceinline__ uint32_t cnt(const Smem& sm, uint32_t region, int v) {
+  return (sm.hist[region + vb_word(v)] >> vb_shift(v)) & 0xFFFFu;
 }
 
-// Block-wide exclusive scan in thread order of (u64, u32); every thread gets
-// its exclusive prefix and the totals.
-__device__ __forceinline__ void block_scan2(Smem& sm, unsigned long long w, uint32_t c,
+// 0xFFFF in the low half when bit 2p of b is set, in the high half when bit
+// 2p + 1 is
+__device__ __forceinline__ uint32_t spread(uint32_t b, int p) {
+  const uint32_t lo = (uint32_t)((int32_t)(b << (31 - 2 * p)) >> 31);
+  const uint32_t hi = (uint32_t)((int32_t)(b << (30 - 2 * p)) >> 31);
+  return (lo & 0xFFFFu) | (hi & 0xFFFF0000u);
+}
+
+// region-A word indices (two 16-bit halves) of a token pair: a saturating
+// subtraction sends zeros and tiny values to index 0, a minimum sends the
+// values above the range (and infinities, NaN) to the escape word
+__device__ __forceinline__ uint32_t pair_words(uint32_t w) {
+  const us2 i = __builtin_elementwise_sub_sat(as_us2(w & 0x7FFF7FFFu), (us2)(unsigned short)(kBase - 1u));
+  return as_u32(__builtin_elementwise_min(i, (us2)(unsigned short)kNI));
+}
+
+__device__ __forceinline__ void lds_add(Smem& sm, uint32_t word, uint32_t v) {
+  __hip_atomic_fetch_add(&sm.hist[word], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Block-wide exclusive scan in thread order of (u64, u32) plus a float sum;
+// every thread gets its exclusive prefix and the totals.
+__device__ __forceinline__ void block_scan2(Smem& sm, unsigned long long w, uint32_t c, float f,
                                             unsigned long long& ew, uint32_t& ec,
-                                            unsigned long long& tw, uint32_t& tc) {
+                                            unsigned long long& tw, uint32_t& tc, float& tf) {
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const unsigned long long iw = wave_scan_u64(w);
   const uint32_t ic = wave_scan_u32(c);
+  const float sf = wave_sum_f(f);
   __syncthreads();
   if (lane == kWave - 1) {
     sm.red_w[wid] = iw;
     sm.red_u[wid][0] = ic;
+    sm.red_f[wid][0] = sf;
   }
   __syncthreads();
   unsigned long long bw = 0ull, allw = 0ull;
   uint32_t bc = 0u, allc = 0u;
+  float allf = 0.0f;
 #pragma unroll
   for (int i = 0; i < kW; ++i) {
     const unsigned long long vw = sm.red_w[i];
@@ -134,123 +205,146 @@ __device__ __forceinline__ void block_scan2(Smem& sm, unsigned long long w, uint
     }
     allw += vw;
     allc += vc;
+    allf += sm.red_f[i][0];
   }
   ew = bw + iw - w;
   ec = bc + ic - c;
   tw = allw;
   tc = allc;
+  tf = allf;
 }
 
-// Block maximum of a u32 (every thread gets it).
-__device__ __forceinline__ uint32_t block_max_u32(Smem& sm, uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  __syncthreads();
-  if (lane == 0) sm.red_u[wid][1] = v;
-  __syncthreads();
-  uint32_t r = sm.red_u[0][1];
-#pragma unroll
-  for (int i = 1; i < kW; ++i) r = sm.red_u[i][1] > r ? sm.red_u[i][1] : r;
-  return r;
-}
-
-template <bool kMask>
 struct Row {
   const uint16_t* __restrict__ x;
   const uint32_t* __restrict__ mask;
   int64_t V, nvec;
-  bool use_pen;
   float rho, Tc;
   // processed logits (contract steps: penalty, then temperature), zeros canonical
-  __device__ __forceinline__ float pen_v(float x) const { return x < 0.0f ? x * rho : x / rho; }
+  __device__ __forceinline__ float pen_v(float v) const { return v < 0.0f ? v * rho : v / rho; }
   __device__ __forceinline__ float y_of(float v) const { return v / Tc + 0.0f; }
-  __device__ __forceinline__ float ybin(int b) const { return y_of(bin_x(b)); }
-  __device__ __forceinline__ float ypen(int p) const { return y_of(pen_v(bin_x(p))); }
+  __device__ __forceinline__ float ybin(int v) const { return y_of(vb_x(v)); }
+  __device__ __forceinline__ float ypen(int v) const { return y_of(pen_v(vb_x(v))); }
   __device__ __forceinline__ bool allowed(int64_t id) const {
-    return !kMask || ((mask[id >> 5] >> (id & 31)) & 1u);
+    return !mask || ((mask[id >> 5] >> (id & 31)) & 1u);
   }
 };
 
-// smallest bin b with ybin(b) >= y (kBins when y is above every bin)
-template <bool kMask>
-__device__ __forceinline__ int ceil_bin(const Row<kMask>& r, float y) {
-  int g = bin_of(bf16_round_up(y * r.Tc));
-  if (g < 0) {
-    int lo = 0, hi = kBins;  // first bin with ybin >= y in [lo, hi]
+// Largest value bin v with ybin(v) >= y (the smallest binned value whose
+// processed logit reaches y), or -1 when y lies above every bin.
+__device__ __forceinline__ int ceil_v(const Row& r, float y) {
+  int v = vb_of(bf16_round_up(y * r.Tc));
+  if (v < 0) {
+    if (!(r.ybin(0) >= y)) return -1;
+    int lo = 0, hi = kNV - 1;  // ybin(lo) >= y; the answer lies in [lo, hi]
     while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (r.ybin(mid) >= y) hi = mid;
-      else lo = mid + 1;
+      const int mid = (lo + hi + 1) >> 1;
+      if (r.ybin(mid) >= y) lo = mid;
+      else hi = mid - 1;
     }
     return lo;
   }
-  while (g > 0 && r.ybin(g - 1) >= y) --g;
-  while (g < kBins && r.ybin(g) < y) ++g;
-  return g;
+  while (v + 1 < kNV && r.ybin(v + 1) >= y) ++v;
+  while (v >= 0 && r.ybin(v) < y) --v;
+  return v;
 }
 
-// Resolve the crossing of `X` (a weight position) inside thread `t`'s range:
-// one wave sorts the range's distinct values by y, scans their weights and
-// finds the value and the position inside it.  `ex_w` / `ex_c` are the
-// weight and count before the range.  Returns false when the range holds too
-// many penalised values (the caller falls back).
-template <bool kMask>
-__device__ __forceinline__ bool resolve_range(const Smem& sm, const Row<kMask>& r, int t, float m,
-                              unsigned long long X, unsigned long long ex_w, uint32_t ex_c,
-                              int pl, int ph, Level& out) {
+// First value bin p in [0, kNV] with ypen(p) <= y (ypen falls as p grows),
+// by the 64 lanes of a wave: rounds of 64 probes narrow 16128 candidates
+// to one in three steps.  Wave-uniform result.
+__device__ __forceinline__ int first_pen_le(const Row& r, float y) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int hi = kBins - 1 - kPer * t;
-  // entries: lanes 0..15 the unpenalised bins hi - lane, lanes 16..61 the
-  // penalised raw bins pl.., lanes 62 / 63 the unpenalised / penalised zeros
-  const int np = ph >= pl ? ph - pl + 1 : 0;
-  if (np > kPenLanes) return false;
-  const int zero_owner = (kBins - 1 - kBins / 2) / kPer;
+  int lo = 0, hi = kNV;  // the answer lies in [lo, hi]
+  while (hi > lo) {
+    const int span = hi - lo;
+    // lane l probes lo + ceil((l + 1) span / 65) - 1: increasing, inside [lo, hi)
+    const int probe = lo + (int)(((int64_t)(lane + 1) * span + 64) / 65) - 1;
+    const bool le = r.ypen(probe) <= y;
+    const unsigned long long hit = __ballot(le);
+    const unsigned long long miss = __ballot(!le);
+    const int nhi = hit ? __builtin_amdgcn_readlane(probe, __builtin_ctzll(hit)) : hi;
+    const int nlo = miss ? __builtin_amdgcn_readlane(probe, 63 - __builtin_clzll(miss)) + 1 : lo;
+    lo = nlo;
+    hi = nhi;
+  }
+  return lo;
+}
+
+// Resolve the crossing of weight position X (one wave): the owning thread
+// from the stored prefixes, then its range's values -- 16 bins and the
+// penalised values whose y lies between them -- ranked by y, scanned, and
+// the position inside the crossing value.  False: the row must be handed
+// over.
+template <int kMode>
+__device__ __forceinline__ bool resolve(const Smem& sm, const Row& r, float m, unsigned long long X,
+                                        Level& out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  // owner: the last thread t with ex.w[t] <= X (ex.w[kOwners] is the total, > X)
+  const unsigned long long b1 = __ballot(sm.x.ex.w[lane * kPer] <= X);
+  const int base = (63 - __builtin_clzll(b1)) * kPer;
+  const unsigned long long b2 = __ballot(lane < kPer && sm.x.ex.w[base + (lane & (kPer - 1))] <= X);
+  const int t = base + (63 - __builtin_clzll(b2));
+  if (t >= kOwners) return false;
+  const unsigned long long ex_w = sm.x.ex.w[t];
+  const uint32_t ex_c = sm.x.ex.c[t];
+  const int v0 = t * kPer;
+  int pa = 0, np = 0;
+  if (kMode & 1) {
+    const float hi_y = r.ybin(v0);
+    pa = first_pen_le(r, hi_y);
+    const int pe = v0 + kPer < kNV ? first_pen_le(r, r.ybin(v0 + kPer)) : kNV;
+    np = pe - pa;
+    if (np > kPenLanes) return false;
+  }
+  // entries: lanes 0..15 the bins v0 + lane (descending), lanes 16.. the
+  // penalised raw bins pa, pa + 1, .. (descending y)
   float y = kNegInf;
   uint32_t c = 0u;
   int kind = -1, ref = -1;
   if (lane < kPer) {
     kind = 0;
-    ref = hi - lane;
-    c = count16(sm.cnt, ref);
+    ref = v0 + lane;
+    c = cnt(sm, 0u, ref);
     y = r.ybin(ref);
   } else if (lane < kPer + np) {
     kind = 1;
-    ref = pl + (lane - kPer);
-    c = count16(sm.pcnt, ref);
+    ref = pa + (lane - kPer);
+    c = cnt(sm, kR2, ref);
     y = r.ypen(ref);
-  } else if (t == zero_owner && lane >= kWave - 2) {
-    kind = lane == kWave - 2 ? 2 : 3;
-    c = lane == kWave - 2 ? sm.zc : sm.pz;
-    y = 0.0f;
   }
   if (c == 0u) {
     y = kNegInf;
     kind = -1;
   }
   const unsigned long long w1 = c ? detexp_fix(y - m) : 0ull;
-  // sort by (y desc, lane asc): rank by counting, then a permute
-  const unsigned long long key = ((unsigned long long)ord32(y) << 32) | (uint32_t)(kWave - 1 - lane);
-  uint32_t rank = 0;
-  for (int j = 0; j < kWave; ++j) {
-    const uint32_t khi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), j);
-    const uint32_t klo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, j);
-    const unsigned long long kk = ((unsigned long long)khi << 32) | klo;
-    rank += kk > key ? 1u : 0u;
+  float ys;
+  uint32_t cs;
+  int kinds, refs;
+  unsigned long long ws;
+  if (kMode & 1) {
+    // rank by (y desc, lane asc) and move every entry to its rank
+    const uint32_t ky = ord32(y);
+    uint32_t rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < kWave; ++j) {
+      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)ky, j);
+      rank += (kj > ky || (kj == ky && j < lane)) ? 1u : 0u;
+    }
+    auto scatter_u32 = [&](uint32_t v) -> uint32_t {
+      return (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)v);
+    };
+    ys = u2f(scatter_u32(f2u(y)));
+    cs = scatter_u32(c);
+    kinds = (int)scatter_u32((uint32_t)kind);
+    refs = (int)scatter_u32((uint32_t)ref);
+    ws = ((unsigned long long)scatter_u32((uint32_t)(w1 >> 32)) << 32) | scatter_u32((uint32_t)w1);
+  } else {
+    // the 16 bins are in descending order already
+    ys = y;
+    cs = c;
+    kinds = kind;
+    refs = ref;
+    ws = w1;
   }
-  // lane `rank` receives this lane's entry (ds_permute scatters by address)
-  auto scatter_u32 = [&](uint32_t v) -> uint32_t {
-    return (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)v);
-  };
-  const float ys = u2f(scatter_u32(f2u(y)));
-  const uint32_t cs = scatter_u32(c);
-  const int kinds = (int)scatter_u32((uint32_t)kind);
-  const int refs = (int)scatter_u32((uint32_t)ref);
-  const unsigned long long ws = ((unsigned long long)scatter_u32((uint32_t)(w1 >> 32)) << 32) |
-                                scatter_u32((uint32_t)w1);
   const unsigned long long iw = wave_scan_u64((unsigned long long)cs * ws);
   const uint32_t ic = wave_scan_u32(cs);
   const unsigned long long rel = X - ex_w;
@@ -258,6 +352,9 @@ __device__ __forceinline__ bool resolve_range(const Smem& sm, const Row<kMask>& 
   if (!past) return false;  // cannot happen: X lies inside the range
   const int e = __builtin_ctzll(past);
   const float ye = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(ys), e));
+  // the zero bins hold zeros and tiny values of one weight but distinct
+  // order: a position inside them goes to the row-wise path
+  if (ye == 0.0f) return false;
   const unsigned long long grp = __ballot(ys == ye && cs != 0u);
   const int gs = __builtin_ctzll(grp);
   const unsigned long long iw_b =
@@ -267,638 +364,858 @@ __device__ __forceinline__ bool resolve_range(const Smem& sm, const Row<kMask>& 
          : 0ull;
   const uint32_t ic_b = gs ? (uint32_t)__builtin_amdgcn_readlane((int)ic, gs - 1) : 0u;
   const bool in_grp = (grp >> lane) & 1ull;
-  // the group's members (at most one unpenalised bin, one penalised bin and
-  // the two zero counts) and its size
-  uint32_t gn = in_grp ? cs : 0u;
-  gn = wave_sum_u32(gn);
-  int ub = -1, pb = -1, zu = 0, zp = 0;
-  const unsigned long long b0 = __ballot(in_grp && kinds == 0);
-  const unsigned long long b1 = __ballot(in_grp && kinds == 1);
-  if (b0) ub = __builtin_amdgcn_readlane(refs, __builtin_ctzll(b0));
-  if (b1) pb = __builtin_amdgcn_readlane(refs, __builtin_ctzll(b1));
-  zu = __ballot(in_grp && kinds == 2) ? 1 : 0;
-  zp = __ballot(in_grp && kinds == 3) ? 1 : 0;
-  const unsigned long long wt = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ws >> 32), e) << 32) |
-                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ws, e);
+  // the group's members (at most one unpenalised and one penalised value)
+  const uint32_t gn = wave_sum_u32(in_grp ? cs : 0u);
+  const unsigned long long bu = __ballot(in_grp && kinds == 0);
+  const unsigned long long bp = __ballot(in_grp && kinds == 1);
+  const int ub = bu ? __builtin_amdgcn_readlane(refs, __builtin_ctzll(bu)) : -1;
+  const int pb = bp ? __builtin_amdgcn_readlane(refs, __builtin_ctzll(bp)) : -1;
+  const unsigned long long wt =
+      ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ws >> 32), e) << 32) |
+      (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ws, e);
   out.y = ye;
-  out.ubin = ub;
-  out.pbin = pb;
-  out.zero_u = zu;
-  out.zero_p = zp;
+  out.hu = ub >= 0 ? vb_bits(ub) : kNone;
+  out.hp = pb >= 0 ? vb_bits(pb) : kNone;
   out.n = gn;
   out.s_before = ex_w + iw_b;
   out.n_before = ex_c + ic_b;
   out.w = wt;
-  const unsigned long long q = (X - out.s_before) / wt;
+  // q = floor((X - s_before) / wt) < gn <= 2^18: a double estimate, then
+  // exact integer corrections (every product stays below X < 2^63)
+  const unsigned long long num = X - out.s_before;
+  unsigned long long q = (unsigned long long)((double)num / (double)wt);
+  while (q > 0 && q * wt > num) --q;
+  while ((q + 1) * wt <= num) ++q;
   out.k = (uint32_t)q;
   return q < gn;
 }
 
-// Level membership of an allowed token with bf16 pattern h.
-__device__ __forceinline__ bool level_has(const Level& L, bool pen, uint32_t h) {
-  if ((h & 0x7FFFu) == 0u) return pen ? L.zero_p != 0 : L.zero_u != 0;
-  return pen ? (L.pbin >= 0 && h == bin_bits(L.pbin)) : (L.ubin >= 0 && h == bin_bits(L.ubin));
+__device__ __forceinline__ bool in_level(const Level& L, bool pn, uint32_t h) {
+  return h == (pn ? L.hp : L.hu);
 }
 
-// Every token of the level is in the pool: each of its values before
-// temperature is at or above theta and above every capture the full pool
-// dropped.
-template <bool kMask>
-__device__ __forceinline__ bool level_in_pool(const Smem& sm, const Row<kMask>& r, const Level& L,
-                                              float theta) {
-  bool ok = true;
-  auto check = [&](float v) {
-    v = v + 0.0f;
-    ok = ok && v >= theta && (sm.drop_key == 0u || ord32(v) > sm.drop_key);
-  };
-  if (L.ubin >= 0) check(bin_x(L.ubin));
-  if (L.pbin >= 0) check(r.pen_v(bin_x(L.pbin)));
-  if (L.zero_u || L.zero_p) check(0.0f);
-  return ok;
-}
-
-// Ids of the two levels' wanted tokens by a rescan of the row (block-wide):
-// pass 1 counts each level's tokens in 16 equal ranges, one per wave; pass 2
-// walks the range that holds the wanted token.  Writes sm.id_out[0..1].
-template <bool kMask>
-__device__ __forceinline__ void rescan_ids(Smem& sm, const Row<kMask>& r) {
+// Ids of the two levels' wanted tokens by one more read of the row: wave w
+// walks the contiguous range w of 16, counts each level's tokens with packed
+// 16-bit compares (bit 15 of a half is set where the half equals the level's
+// pattern), keeps up to kRescanBuf matching ids per level in id order; the
+// wave whose range holds a wanted token reads it from its buffer, or walks
+// its range again when the buffer overflowed.  Writes sm.id_out[0..1].
+template <int kMode>
+__device__ __forceinline__ void rescan_ids(Smem& sm, const Row& r) {
+  constexpr bool kPen = (kMode & 1) != 0, kMask = (kMode & 2) != 0;
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const int64_t nvec = r.nvec, V = r.V;
   const int64_t span = (nvec + kW - 1) / kW;
-  const int64_t v0 = wid * span, v1 = v0 + span < nvec ? v0 + span : nvec;
+  const int64_t v0 = wid * span < nvec ? wid * span : nvec;
+  const int64_t v1 = v0 + span < nvec ? v0 + span : nvec;
   const Level L0 = sm.lv[0], L1 = sm.lv[1];
-  // matches of one vector (or, for v == nvec, of the tail tokens), as two 8-bit masks
-  auto vec_matches = [&](int64_t v, uint32_t& m0, uint32_t& m1) __attribute__((always_inline)) {
-    m0 = m1 = 0u;
-    if (v < nvec) {
-      const u32x4 q = *reinterpret_cast<const u32x4*>(r.x + v * 8);
-      const uint32_t wds[4] = {q.x, q.y, q.z, q.w};
-      const uint32_t ab = kMask ? (r.mask[v >> 2] >> ((v & 3) * 8)) & 0xFFu : 0xFFu;
-      const uint32_t pb = r.use_pen ? (sm.pen[v >> 2] >> ((v & 3) * 8)) & 0xFFu : 0u;
+  uint32_t* buf0 = sm.hist + (0 * kW + wid) * kRescanBuf;
+  uint32_t* buf1 = sm.hist + (1 * kW + wid) * kRescanBuf;
+  // a level's value in both halves (0xFFFF, a NaN pattern, matches nothing
+  // here: such rows never reach this point)
+  auto pat = [](uint32_t h) { return h == kNone ? 0xFFFFFFFFu : h * 0x10001u; };
+  const uint32_t u0 = pat(L0.hu), p0 = pat(L0.hp), u1 = pat(L1.hu), p1 = pat(L1.hp);
+  auto zeq = [](uint32_t w, uint32_t pt) {
+    const uint32_t x = w ^ pt;
+    return as_u32(as_us2(x) - (us2)(unsigned short)1) & ~x & 0x80008000u;
+  };
+  // match bits (15 and 31 of each word) of vector v for both levels
+  auto matches = [&](int64_t v, const u32x4& q, uint32_t(&m0)[4], uint32_t(&m1)[4])
+                     __attribute__((always_inline)) {
+    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t ab = kMask ? (r.mask[v >> 2] >> ((v & 3) * 8)) & 0xFFu : 0xFFu;
+    const uint32_t pb = kPen ? (sm.pen()[v >> 2] >> ((v & 3) * 8)) & 0xFFu : 0u;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t h = (j & 1) ? wds[j >> 1] >> 16 : wds[j >> 1] & 0xFFFFu;
-        const bool on = (ab >> j) & 1u, pn = (pb >> j) & 1u;
-        m0 |= (on && level_has(L0, pn, h)) ? 1u << j : 0u;
-        m1 |= (on && level_has(L1, pn, h)) ? 1u << j : 0u;
-      }
-    } else {
-      for (int64_t id = nvec * 8; id < V; ++id) {
-        const int j = (int)(id - nvec * 8);
-        const uint32_t h = r.x[id];
-        const bool on = r.allowed(id);
-        const bool pn = r.use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
-        m0 |= (on && level_has(L0, pn, h)) ? 1u << j : 0u;
-        m1 |= (on && level_has(L1, pn, h)) ? 1u << j : 0u;
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t a2 = kMask ? spread(ab, p) & 0x80008000u : 0x80008000u;
+      if (kPen) {
+        const uint32_t pn2 = spread(pb, p) & 0x80008000u;
+        m0[p] = ((zeq(wd[p], u0) & ~pn2) | (zeq(wd[p], p0) & pn2)) & a2;
+        m1[p] = ((zeq(wd[p], u1) & ~pn2) | (zeq(wd[p], p1) & pn2)) & a2;
+      } else {
+        m0[p] = zeq(wd[p], u0) & a2;
+        m1[p] = zeq(wd[p], u1) & a2;
       }
     }
   };
+  auto bits8 = [](const uint32_t(&m)[4]) {
+    uint32_t b = 0u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) b |= (((m[p] >> 15) & 1u) << (2 * p)) | ((m[p] >> 31) << (2 * p + 1));
+    return b;
+  };
+  auto count4 = [](const uint32_t(&m)[4]) {
+    return (uint32_t)(__builtin_popcount(m[0]) + __builtin_popcount(m[1]) + __builtin_popcount(m[2]) +
+                      __builtin_popcount(m[3]));
+  };
+  auto tail_matches = [&](uint32_t& t0, uint32_t& t1) {
+    t0 = t1 = 0u;
+    for (int64_t id = nvec * 8; id < V; ++id) {
+      const int j = (int)(id - nvec * 8);
+      const uint32_t h = r.x[id];
+      const bool on = r.allowed(id);
+      const bool pn = kPen && ((sm.pen()[id >> 5] >> (id & 31)) & 1u);
+      t0 |= (on && in_level(L0, pn, h)) ? 1u << j : 0u;
+      t1 |= (on && in_level(L1, pn, h)) ? 1u << j : 0u;
+    }
+  };
   const bool has_tail = wid == kW - 1 && nvec * 8 < V;
-  // pass 1
-  uint32_t c0 = 0u, c1 = 0u;
-  for (int64_t v = v0 + lane; v < v1; v += kWave) {
-    uint32_t m0, m1;
-    vec_matches(v, m0, m1);
-    c0 += __builtin_popcount(m0);
-    c1 += __builtin_popcount(m1);
+  constexpr int64_t kStep = (int64_t)kWave * kRescanG;
+  // append the set bits of mm (ids base + bit) at position ex onwards
+  auto keep = [&](uint32_t* buf, uint32_t mm, uint32_t ex, int64_t base) {
+    uint32_t i = ex;
+    while (mm) {
+      const int j = __builtin_ctz(mm);
+      mm &= mm - 1u;
+      if (i < (uint32_t)kRescanBuf) buf[i] = (uint32_t)(base + j);
+      ++i;
+    }
+  };
+  uint32_t run0 = 0u, run1 = 0u;
+  for (int64_t vb = v0; vb < v1; vb += kStep) {
+    u32x4 q[kRescanG];
+#pragma unroll
+    for (int g = 0; g < kRescanG; ++g) {
+      const int64_t v = vb + g * kWave + lane;
+      q[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(r.x) + (v < v1 ? v : v0));
+    }
+#pragma unroll
+    for (int g = 0; g < kRescanG; ++g) {
+      const int64_t v = vb + g * kWave + lane;
+      uint32_t m0[4] = {0u, 0u, 0u, 0u}, m1[4] = {0u, 0u, 0u, 0u};
+      if (v < v1) matches(v, q[g], m0, m1);
+      const uint32_t n0 = count4(m0), n1 = count4(m1);
+      if (!__ballot((n0 | n1) != 0u)) continue;
+      const uint32_t i0 = wave_scan_u32(n0), i1 = wave_scan_u32(n1);
+      if (n0) keep(buf0, bits8(m0), run0 + i0 - n0, v * 8);
+      if (n1) keep(buf1, bits8(m1), run1 + i1 - n1, v * 8);
+      run0 += lane63_u32(i0);
+      run1 += lane63_u32(i1);
+    }
   }
-  if (has_tail && lane == 0) {
-    uint32_t m0, m1;
-    vec_matches(nvec, m0, m1);
-    c0 += __builtin_popcount(m0);
-    c1 += __builtin_popcount(m1);
+  if (has_tail) {
+    uint32_t t0, t1;
+    tail_matches(t0, t1);
+    if (lane == 0) {
+      keep(buf0, t0, run0, nvec * 8);
+      keep(buf1, t1, run1, nvec * 8);
+    }
+    run0 += __builtin_popcount(t0);
+    run1 += __builtin_popcount(t1);
   }
-  c0 = wave_sum_u32(c0);
-  c1 = wave_sum_u32(c1);
   if (lane == 0) {
-    sm.scan_n[wid][0] = c0;
-    sm.scan_n[wid][1] = c1;
+    sm.scan_n[wid][0] = run0;
+    sm.scan_n[wid][1] = run1;
   }
   __syncthreads();
-  // pass 2: the wave whose range holds the wanted token of a level finds it
   for (int l = 0; l < 2; ++l) {
     const uint32_t k = l ? L1.k : L0.k;
     uint32_t before = 0u;
     for (int w = 0; w < wid; ++w) before += sm.scan_n[w][l];
-    if (!(before <= k && k < before + sm.scan_n[wid][l])) continue;
-    uint32_t run = before;
-    for (int64_t vb = v0; vb < v1 + (has_tail ? 1 : 0); vb += kWave) {
+    const uint32_t mine = sm.scan_n[wid][l];
+    if (!(before <= k && k < before + mine)) continue;
+    const uint32_t local = k - before;
+    if (mine <= (uint32_t)kRescanBuf) {
+      if (lane == 0) sm.id_out[l] = (int32_t)(l ? buf1 : buf0)[local];
+      continue;
+    }
+    // the buffer overflowed: walk the range again up to the wanted match
+    uint32_t run = 0u;
+    bool done = false;
+    for (int64_t vb = v0; vb < v1 && !done; vb += kWave) {
       const int64_t v = vb + lane;
-      uint32_t m0 = 0u, m1 = 0u;
-      if (v < v1 || (has_tail && v == nvec)) vec_matches(v, m0, m1);
-      const uint32_t mm = l ? m1 : m0;
+      uint32_t m0[4] = {0u, 0u, 0u, 0u}, m1[4] = {0u, 0u, 0u, 0u};
+      if (v < v1) matches(v, *reinterpret_cast<const u32x4*>(r.x + v * 8), m0, m1);
+      const uint32_t mm = l ? bits8(m1) : bits8(m0);
       const uint32_t n = __builtin_popcount(mm);
       const uint32_t incl = wave_scan_u32(n);
-      const uint32_t tot = lane63_u32(incl);
-      if (run + tot > k) {
-        const uint32_t ex = run + incl - n;
-        if (n && ex <= k && k < ex + n) {
-          uint32_t mk = mm;
-          for (uint32_t i = 0; i < k - ex; ++i) mk &= mk - 1u;
-          sm.id_out[l] = (int32_t)(v * 8 + __builtin_ctz(mk));
-        }
-        break;
+      const uint32_t ex = run + incl - n;
+      if (n && ex <= local && local < ex + n) {
+        uint32_t mk = mm;
+        for (uint32_t i = 0; i < local - ex; ++i) mk &= mk - 1u;
+        sm.id_out[l] = (int32_t)(v * 8 + __builtin_ctz(mk));
       }
-      run += tot;
+      run += lane63_u32(incl);
+      done = run > local;
+    }
+    if (!done && has_tail && lane == 0) {  // the wanted token is in the tail
+      uint32_t t0, t1;
+      tail_matches(t0, t1);
+      uint32_t mm = l ? t1 : t0;
+      for (uint32_t i = 0; i < local - run; ++i) mm &= mm - 1u;
+      sm.id_out[l] = (int32_t)(nvec * 8 + __builtin_ctz(mm));
     }
   }
   __syncthreads();
 }
 
-// One row; false when the row needs the row-wise path (a block-uniform
-// decision, taken before any output is written).
-template <bool kMask>
+// One row; false when the row must be handed over to the row-wise path (a
+// block-uniform decision, taken before any output is written).
+// kMode bit 0: repetition penalty; bit 1: allow mask.
+template <int kMode>
 __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& sm) {
+  constexpr bool kPen = (kMode & 1) != 0, kMask = (kMode & 2) != 0;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
-  Row<kMask> r;
+  Row r;
   r.x = reinterpret_cast<const uint16_t*>(a.logits) + b * a.row_stride;
   r.mask = kMask ? a.mask + b * a.mask_stride : nullptr;
   r.V = a.V;
   r.nvec = a.V / 8;
-  r.use_pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
   r.rho = a.rho;
   r.Tc = a.T > 1e-6f ? a.T : 1e-6f;
   const float u = a.uniforms[b];
   const int64_t V = a.V, nvec = r.nvec;
   const uint32_t nchunks = (uint32_t)((nvec + kChunk - 1) / kChunk);
   const uint32_t per = nchunks / kW;
+  const bool ragged = (nvec % kChunk) != 0;  // the last chunk is partial
   // chunk c of the dynamic schedule -> chunk of the row: the first kW chunks
   // handed out start kW evenly spaced regions (the pilot sample)
   auto perm = [&](uint32_t c) -> uint32_t { return c < per * kW ? (c % kW) * per + c / kW : c; };
+  // a thread's 16 bins are 16 consecutive words: visited in a per-thread
+  // rotated order, the 64 lanes of a wave hit distinct LDS banks
+  auto rot = [&](int j) -> int { return (j + (tid >> 2)) & (kPer - 1); };
 
-  // ---- 0. clear
-  for (int i = tid; i < kBins / 2; i += kB) {
-    sm.cnt[i] = 0u;
-    sm.pcnt[i] = 0u;
-  }
-  if (r.use_pen)
-    for (int64_t i = tid; i < (V + 31) / 32; i += kB) sm.pen[i] = 0u;
-  if (tid < 512) sm.sel[tid >> 8][tid & 255] = 0u;
-  if (tid == 0) {
-    sm.owner[0] = -1;
-    sm.owner[1] = -1;
-    sm.chunk_ctr = 0u;
-    sm.pool_n = 0u;
-    sm.drop_key = 0u;
-    sm.n_counted = 0u;
-    sm.zc = 0u;
-    sm.pz = 0u;
-    sm.flags = 0u;
-    sm.bad = 0;
-  }
-  __syncthreads();
-
-  // ---- 1. the first two chunks in flight, then the history bitmap
+  // ---- 0. the first two chunks of each wave in flight (chunks w and kW + w
+  // of the schedule), then the clear
   const uint32_t last = (uint32_t)(nvec - 1);
   const uint32_t last_word = (uint32_t)((V - 1) >> 5);
-  auto grab = [&]() -> uint32_t {
-    uint32_t c = 0;
-    if (lane == 0) c = atomicAdd(&sm.chunk_ctr, 1u);
-    return __builtin_amdgcn_readfirstlane(c);
-  };
   auto issue = [&](u32x4(&buf)[kG], uint32_t& sw, uint32_t chunk) {
-    const uint32_t pc = chunk < nchunks ? perm(chunk) : 0u;
+    const uint32_t pc = perm(chunk);
 #pragma unroll
     for (int k = 0; k < kG; ++k) {
       uint32_t vi = pc * kChunk + (uint32_t)(k * kWave + lane);
       vi = vi < last ? vi : last;
       buf[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(r.x) + vi);
     }
-    if (kMask) {  // the chunk's 32 mask words, one per lane (lanes 32..63 repeat them)
-      uint32_t w = pc * (kChunk * 8 / 32) + (uint32_t)(lane & 31);
+    if (kMask) {  // the chunk's 64 mask words, one per lane
+      const uint32_t w = pc * (kChunk * 8 / 32) + (uint32_t)lane;
       sw = r.mask[w < last_word ? w : last_word];
     }
   };
   u32x4 qa[kG], qb[kG];
   uint32_t swa = 0xFFFFFFFFu, swb = 0xFFFFFFFFu;
-  uint32_t ca = grab();
-  issue(qa, swa, ca);
-  uint32_t cb = grab();
-  issue(qb, swb, cb);
-  bool bad_hist = false;
+  uint32_t ca = (uint32_t)wid, cb = (uint32_t)(kW + wid);
+  if (ca < nchunks) issue(qa, swa, ca);
+  if (cb < nchunks) issue(qb, swb, cb);
+  {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < kHistWords / 4; i += kB) reinterpret_cast<u32x4*>(sm.hist)[i] = z;
+    if (kPen)
+      for (int64_t i = tid; i < (V + 127) / 128; i += kB) reinterpret_cast<u32x4*>(sm.pen())[i] = z;
+  }
+  if (tid == 0) {
+    sm.chunk_ctr = 2u * kW;
+    sm.pool_n = 0u;
+    sm.drop_ord = 0u;
+    sm.theta = kNone;
+    sm.flags = 0u;
+    sm.bad = 0;
+    sm.list_n[0] = 0u;
+    sm.list_n[1] = 0u;
+    sm.id_out[0] = -1;
+    sm.id_out[1] = -1;
+  }
+  __syncthreads();
+
+  // ---- 1. the history bitmap
+  auto grab = [&]() -> uint32_t {
+    uint32_t c = 0;
+    if (lane == 0) c = atomicAdd(&sm.chunk_ctr, 1u);
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)c);
+  };
   if (a.hist && a.hist_len > 0) {
     const int32_t* h = a.hist + b * a.hist_stride;
+    bool bad_hist = false;
     for (int64_t j = tid; j < a.hist_len; j += kB) {
       const int32_t id = h[j];
       if (id >= V) bad_hist = true;
-      else if (id >= 0 && r.use_pen) atomicOr(&sm.pen[id >> 5], 1u << (id & 31));
+      else if (kPen && id >= 0) atomicOr(&sm.pen()[id >> 5], 1u << (id & 31));
     }
+    if (bad_hist) atomicOr(&sm.flags, 2u);
   }
-  if (bad_hist) atomicOr(&sm.flags, 2u);
+  __syncthreads();  // the history bitmap is complete
 
   // allow bits of vector k of a chunk for this lane (vector k*64 + lane); a
-  // cross-lane read, so every lane of the wave calls it (a lane past the
-  // row's end would otherwise hand its neighbours a zero byte)
+  // cross-lane read, so every lane of the wave calls it
   auto allow_byte = [&](uint32_t sw, int k) -> uint32_t {
-    if (!kMask) return 0xFFu;
     const uint32_t w = (uint32_t)__shfl((int)sw, k * (kWave / 4) + lane / 4, kWave);
     return (w >> ((lane & 3) * 8)) & 0xFFu;
   };
 
-  // ---- 2. pilot: theta from the first chunk of every wave
-  {
-    uint32_t keys[kG][8];
+  // ---- 2. stream state and a chunk's work
+  Lse3 st{kNegInf, 0.0f, 0.0f};  // raw log-sum-exp per token (mask and penalty)
+  const uint32_t junk2 = kJunk * 0x10001u;
+  const uint32_t spill2 = (kSpill + (uint32_t)lane) * 0x10001u;
+  // capture test: signed 16-bit compare of the raw bits against a theta >= 0,
+  // order keys otherwise
+  bool cap_signed = false;
+  uint32_t cap_th2 = 0u;  // theta - 1 (signed) or ord16(theta) - 1, in both halves
+  int th_s = 0;           // theta as a signed 16-bit pattern
+  uint32_t th_o = 1u;     // ord16(theta) (1: every allowed token)
+  uint32_t rmax = 0u;     // running maximum of the allowed tokens (packed, test's domain)
+  constexpr uint32_t kCap = kPen ? kPoolVPen : kPoolV;
+  // a vector whose test passed goes whole into the pool (one LDS atomic per
+  // wave and step); a full pool keeps the largest key it dropped
+  auto append = [&](bool c, uint32_t vi, const u32x4& vec, uint32_t ab) __attribute__((always_inline)) {
+    const unsigned long long bal = __ballot(c);
+    if (!bal) return;
+    uint32_t base = 0u;
+    if (lane == 0) base = atomicAdd(&sm.pool_n, (uint32_t)__builtin_popcountll(bal));
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+    if (c) {
+      const uint32_t slot = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (slot < kCap) {
+        sm.qd[slot] = vec;
+        sm.qv[slot] = (uint16_t)vi;
+      } else {
+        const uint32_t wd[4] = {vec.x, vec.y, vec.z, vec.w};
+        uint32_t mo = 0u;
 #pragma unroll
-    for (int k = 0; k < kG; ++k) {
-      const uint32_t pc = perm(ca);
-      const uint32_t vi = pc * kChunk + (uint32_t)(k * kWave + lane);
-      const uint32_t ab_all = allow_byte(swa, k);
-      const uint32_t ab = vi < (uint32_t)nvec ? ab_all : 0u;
-      const uint32_t wds[4] = {qa[k].x, qa[k].y, qa[k].z, qa[k].w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t h = (j & 1) ? wds[j >> 1] >> 16 : wds[j >> 1] & 0xFFFFu;
-        keys[k][j] = ((ab >> j) & 1u) ? ord16(h) : 0u;
-        if (keys[k][j]) atomicAdd(&sm.sel[0][keys[k][j] >> 8], 1u);
-      }
-    }
-    const uint32_t ks = (uint32_t)(((uint64_t)kTarget * (uint64_t)(kW * kChunk * 8) + (uint64_t)V - 1) /
-                                   (uint64_t)V);
-    __syncthreads();  // also completes the history bitmap
-    auto pick = [&](const uint32_t* hist, uint32_t want, uint32_t& bin, uint32_t& rem) {
-      // descending over 256 bins, 4 per lane: the bin holding the want-th key
-      uint32_t c[4], s4 = 0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        c[i] = hist[255 - 4 * lane - i];
-        s4 += c[i];
-      }
-      const uint32_t incl = wave_scan_u32(s4);
-      const unsigned long long hit = __ballot(incl >= want);
-      bin = 0xFFFFFFFFu;
-      rem = 0u;
-      if (!hit) return;
-      const int l = __builtin_ctzll(hit);
-      if (lane == l) {
-        uint32_t run = incl - s4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (bin == 0xFFFFFFFFu && run + c[i] >= want) {
-            bin = (uint32_t)(255 - 4 * lane - i);
-            rem = want - run;
-          }
-          run += c[i];
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t h = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
+          const uint32_t k = ((ab >> j) & 1u) ? ord16(h) : 0u;
+          mo = k > mo ? k : mo;
         }
-      }
-      bin = (uint32_t)__builtin_amdgcn_readlane((int)bin, l);
-      rem = (uint32_t)__builtin_amdgcn_readlane((int)rem, l);
-    };
-    if (wid == 0) {
-      uint32_t hb, rem;
-      pick(sm.sel[0], ks, hb, rem);
-      if (lane == 0) {
-        sm.theta_sel[0] = hb;
-        sm.theta_sel[1] = rem;
+        atomicMax(&sm.drop_ord, mo);
       }
     }
-    __syncthreads();
-    const uint32_t hb = sm.theta_sel[0];
-    if (hb != 0xFFFFFFFFu) {
-#pragma unroll
-      for (int k = 0; k < kG; ++k)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (keys[k][j] && (keys[k][j] >> 8) == hb) atomicAdd(&sm.sel[1][keys[k][j] & 0xFFu], 1u);
-    }
-    __syncthreads();
-    if (wid == 0 && hb != 0xFFFFFFFFu) {
-      uint32_t lb, rem2;
-      pick(sm.sel[1], sm.theta_sel[1], lb, rem2);
-      if (lane == 0) sm.theta_sel[0] = (hb << 8) | lb;
-    } else if (wid == 0 && lane == 0) {
-      sm.theta_sel[0] = 0xFFFFFFFFu;  // fewer allowed sample tokens than wanted: capture all
-    }
-    __syncthreads();
-  }
-  const uint32_t tkey = sm.theta_sel[0];
-  const float theta = tkey == 0xFFFFFFFFu ? kNegInf : u2f(unord16(tkey) << 16);
-  // vectors whose maximum is below th_lo hold no capture (rho < 1 lifts
-  // penalised values, so there every vector is tested)
-  const float th_lo = (r.use_pen && r.rho < 1.0f) ? kNegInf : theta;
-
-  // ---- 3. stream
-  Lse3 st{kNegInf, 0.0f, 0.0f};
-  uint32_t counted = 0u;
-  bool spill = false;
-  auto count_token = [&](uint32_t h, bool pn) __attribute__((always_inline)) {
-    const int bn = bin_of(h);
-    if (bn >= 0) {
-      atomicAdd((pn ? sm.pcnt : sm.cnt) + (bn >> 1), 1u << ((bn & 1) * 16));
-      ++counted;
-    } else if ((h & 0x7FFFu) == 0u) {
-      atomicAdd(pn ? &sm.pz : &sm.zc, 1u);
-    } else if (h != 0xFF80u) {
-      spill = true;  // NaN, +inf, or a value outside the bins
-    }
   };
-  auto capture = [&](uint32_t id, uint32_t h, bool pn, uint32_t slot, float v) __attribute__((always_inline)) {
-    if (slot < (uint32_t)kPool) {
-      sm.qid[slot] = id | (pn ? 0x80000000u : 0u);
-      sm.qh[slot] = (uint16_t)h;
-    } else {
-      atomicMax(&sm.drop_key, ord32(v + 0.0f));
-    }
-  };
-  auto consume = [&](const u32x4(&buf)[kG], uint32_t sw, uint32_t chunk) __attribute__((always_inline)) {
+  // (partial, count, capture arrive as integral constants: each combination
+  // compiles to its own branch-free body)
+  auto work = [&](const u32x4(&buf)[kG], uint32_t sw, uint32_t chunk, auto partial_c, auto count_c,
+                  auto capture_c) __attribute__((always_inline)) {
+    constexpr bool partial = decltype(partial_c)::value;
+    constexpr bool count = decltype(count_c)::value;
+    constexpr bool capture = decltype(capture_c)::value;
     const uint32_t pc = perm(chunk);
-    float x[kG][8], vm[kG];
-#pragma unroll
-    for (int k = 0; k < kG; ++k) {
-      Vec<uint16_t>::cvt(buf[k], x[k]);
-      const uint32_t vi = pc * kChunk + (uint32_t)(k * kWave + lane);
-      if (vi >= (uint32_t)nvec) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[k][j] = kNegInf;
-      }
-      vm[k] = vec_max<8>(x[k]);
-    }
-    float cm = vm[0];
-#pragma unroll
-    for (int k = 1; k < kG; ++k) cm = max3raw(cm, vm[k], vm[k]);
-    lse_fold_block_max<false, kG, 8>(st, x, cm);
+    float xf[kG][8];
+    float cm = kNegInf;
 #pragma unroll
     for (int k = 0; k < kG; ++k) {
       const uint32_t vi = pc * kChunk + (uint32_t)(k * kWave + lane);
-      const uint32_t ab_all = allow_byte(sw, k);
-      const uint32_t ab = vi < (uint32_t)nvec ? ab_all : 0u;
-      const uint32_t pb = r.use_pen ? (sm.pen[(vi < last ? vi : last) >> 2] >> ((vi & 3) * 8)) & 0xFFu : 0u;
-      const uint32_t wds[4] = {buf[k].x, buf[k].y, buf[k].z, buf[k].w};
+      const bool valid = !partial || vi < (uint32_t)nvec;  // (always true for full chunks)
+      uint32_t ab = kMask ? allow_byte(sw, k) : 0xFFu;
+      if (partial && !valid) ab = 0u;
+      const uint32_t pb =
+          kPen ? (sm.pen()[(vi < last ? vi : last) >> 2] >> ((vi & 3) * 8)) & 0xFFu : 0u;
+      const uint32_t wd[4] = {buf[k].x, buf[k].y, buf[k].z, buf[k].w};
+      uint32_t mk[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t h = (j & 1) ? wds[j >> 1] >> 16 : wds[j >> 1] & 0xFFFFu;
-        if ((ab >> j) & 1u) count_token(h, (pb >> j) & 1u);
-      }
-      uint32_t cap = 0u;
-      if (ab && vm[k] >= th_lo) {
+      for (int p = 0; p < 4; ++p) mk[p] = (kMask || partial) ? spread(ab, p) : 0xFFFFFFFFu;
+      if constexpr (count) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = ((pb >> j) & 1u) ? r.pen_v(x[k][j]) : x[k][j];
-          cap |= (((ab >> j) & 1u) && v >= theta) ? 1u << j : 0u;
-        }
-      }
-      if (__ballot(cap != 0u)) {
-        const uint32_t n = __builtin_popcount(cap);
-        const uint32_t incl = wave_scan_u32(n);
-        uint32_t base = 0u;
-        if (lane == 0) base = atomicAdd(&sm.pool_n, lane63_u32(incl));
-        else (void)lane63_u32(incl);
-        base = __builtin_amdgcn_readfirstlane(base);
-        uint32_t slot = base + incl - n;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if ((cap >> j) & 1u) {
-            const uint32_t h = (j & 1) ? wds[j >> 1] >> 16 : wds[j >> 1] & 0xFFFFu;
-            const bool pn = (pb >> j) & 1u;
-            capture(vi * 8u + (uint32_t)j, h, pn, slot, pn ? r.pen_v(x[k][j]) : x[k][j]);
-            ++slot;
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t w = wd[p];
+          uint32_t a2 = pair_words(w);  // region 2: + kR2 (bit 13 of each half)
+          if (kMode == 1) a2 |= spread(pb, p) & 0x20002000u;
+          if (kMode == 2) a2 |= ~mk[p] & 0x20002000u;
+          if (kMode == 3) {
+            a2 |= spread(pb, p) & 0x20002000u;
+            a2 = (a2 & mk[p]) | (spill2 & ~mk[p]);
           }
+          if (partial && !valid) a2 = junk2;
+          // a negative value counts in the high half: 1 + 0xFFFF per negative token
+          const uint32_t neg = as_u32(as_ss2(w) >> (ss2)(short)15);
+          lds_add(sm, a2 & 0xFFFFu, (neg & 0xFFFFu) + 1u);
+          lds_add(sm, a2 >> 16, (neg >> 16) + 1u);
+        }
+        if constexpr (kMode == 3) {
+          Vec<uint16_t>::cvt(buf[k], xf[k]);
+          if (partial && !valid) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xf[k][j] = kNegInf;
+          }
+          cm = max3raw(cm, vec_max<8>(xf[k]), kNegInf);
         }
       }
+      if constexpr (capture) {
+        bool c;
+        if (cap_signed) {
+          ss2 mx;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t q = (kMask || partial) ? ((wd[p] & mk[p]) | (0x80008000u & ~mk[p])) : wd[p];
+            mx = p ? __builtin_elementwise_max(mx, as_ss2(q)) : as_ss2(q);
+          }
+          rmax = as_u32(__builtin_elementwise_max(as_ss2(rmax), mx));
+          mx = __builtin_elementwise_max(mx, as_ss2(cap_th2));
+          c = as_u32(mx) != cap_th2;
+        } else {
+          us2 mx;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t neg = as_u32(as_ss2(wd[p]) >> (ss2)(short)15);
+            uint32_t q = wd[p] ^ (neg | 0x80008000u);
+            if (kMask || partial) q &= mk[p];
+            mx = p ? __builtin_elementwise_max(mx, as_us2(q)) : as_us2(q);
+          }
+          rmax = as_u32(__builtin_elementwise_max(as_us2(rmax), mx));
+          mx = __builtin_elementwise_max(mx, as_us2(cap_th2));
+          c = as_u32(mx) != cap_th2;
+        }
+        append(c, vi, buf[k], ab);
+      }
     }
+    if constexpr (kMode == 3 && count) lse_fold_block_max<false, kG, 8>(st, xf, cm);
   };
-  while (ca < nchunks) {
-    consume(qa, swa, ca);
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  auto run = [&](const u32x4(&buf)[kG], uint32_t sw, uint32_t chunk, auto count_c, auto capture_c)
+                 __attribute__((always_inline)) {
+    if (ragged && perm(chunk) == nchunks - 1) work(buf, sw, chunk, T_{}, count_c, capture_c);
+    else work(buf, sw, chunk, F_{}, count_c, capture_c);
+  };
+
+  // ---- 3. pilot: count each wave's first chunk, pick theta from the counts
+  if (ca < nchunks) run(qa, swa, ca, T_{}, F_{});
+  __syncthreads();
+  {
+    const int64_t sampled = (int64_t)(nchunks < (uint32_t)kW ? nchunks : (uint32_t)kW) * kChunk * 8;
+    const uint64_t sample = (uint64_t)(sampled < V ? sampled : V);
+    const uint32_t ks =
+        (uint32_t)(((uint64_t)(kPen ? kTargetPen : kTarget) * sample + (uint64_t)V - 1) / (uint64_t)V);
+    uint32_t s = 0u;
+    if (tid < kOwners) {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int v = tid * kPer + rot(j);
+        s += cnt(sm, 0u, v) + (kPen ? cnt(sm, kR2, v) : 0u);
+      }
+    }
+    const uint32_t incl = wave_scan_u32(s);
+    if (lane == kWave - 1) sm.red_u[wid][0] = incl;
+    __syncthreads();
+    uint32_t ex = incl - s;
+#pragma unroll
+    for (int i = 0; i < kW; ++i) ex += i < wid ? sm.red_u[i][0] : 0u;
+    if (ex < ks && ks <= ex + s) {
+      uint32_t run_c = ex;
+      int vt = -1;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        run_c += cnt(sm, 0u, tid * kPer + j) + (kPen ? cnt(sm, kR2, tid * kPer + j) : 0u);
+        if (vt < 0 && run_c >= ks) vt = tid * kPer + j;
+      }
+      sm.theta = vb_bits(vt);
+    }
+    __syncthreads();
+    const uint32_t th = sm.theta;
+    if (th != kNone && !(th & 0x8000u)) {
+      cap_signed = true;
+      th_s = (int)th;
+      cap_th2 = (th - 1u) * 0x10001u;
+      rmax = 0x80008000u;
+    } else {
+      th_o = th == kNone ? 1u : ord16(th);
+      cap_th2 = (th_o - 1u) * 0x10001u;
+      rmax = 0u;
+    }
+  }
+  if (ca < nchunks) run(qa, swa, ca, F_{}, T_{});
+
+  // ---- 4. stream (chunk A of the pilot is done; B is in flight)
+  while (true) {
     if (cb >= nchunks) break;
     ca = grab();
-    issue(qa, swa, ca);
-    consume(qb, swb, cb);
-    cb = grab();
+    if (ca < nchunks) issue(qa, swa, ca);
+    run(qb, swb, cb, T_{}, T_{});
     if (ca >= nchunks) break;
-    issue(qb, swb, cb);
+    cb = grab();
+    if (cb < nchunks) issue(qb, swb, cb);
+    run(qa, swa, ca, T_{}, T_{});
   }
-  if (cb < nchunks && ca >= nchunks) consume(qb, swb, cb);
-  // tail tokens (V not a multiple of 8)
-  for (int64_t id = nvec * 8 + tid; id < V; id += kB) {
-    const uint32_t h = r.x[id];
-    const float xv = u2f(h << 16);
-    float x1[1][4] = {{xv, kNegInf, kNegInf, kNegInf}};
-    lse_fold_block_max<false, 1, 4>(st, x1, xv);
-    if (r.allowed(id)) {
-      const bool pn = r.use_pen && ((sm.pen[id >> 5] >> (id & 31)) & 1u);
-      count_token(h, pn);
-      const float v = pn ? r.pen_v(xv) : xv;
-      if (v >= theta) capture((uint32_t)id, h, pn, atomicAdd(&sm.pool_n, 1u), v);
+  // tail tokens (V not a multiple of 8): lane 0 of wave 0, one token at a
+  // time; the tail is vector nvec (padded with -inf) in the pool
+  if (wid == 0 && nvec * 8 < V && lane == 0) {
+    float xt[1][8];
+    uint32_t wt[4] = {0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u};
+    uint32_t abt = 0u, mo = 0u;
+    for (int j = 0; j < 8; ++j) {
+      const int64_t id = nvec * 8 + j;
+      xt[0][j] = kNegInf;
+      if (id >= V) continue;
+      const uint32_t h = r.x[id];
+      xt[0][j] = u2f(h << 16);
+      wt[j >> 1] = (j & 1) ? (wt[j >> 1] & 0xFFFFu) | (h << 16) : (wt[j >> 1] & 0xFFFF0000u) | h;
+      const bool on = r.allowed(id);
+      const bool pn = kPen && ((sm.pen()[id >> 5] >> (id & 31)) & 1u);
+      uint32_t wi = pair_words(h) & 0xFFFFu;
+      if (kMode == 1 && pn) wi |= kR2;
+      if (kMode == 2 && !on) wi |= kR2;
+      if (kMode == 3) wi = on ? (wi | (pn ? kR2 : 0u)) : kSpill;
+      lds_add(sm, wi, 1u + 0xFFFFu * ((h >> 15) & 1u));
+      if (!on) continue;
+      const uint32_t key = ord16(h);
+      if (cap_signed) {
+        const int hv = (int)(short)h;
+        const int rv = (int)(short)(rmax & 0xFFFFu);
+        if (hv > rv) rmax = (rmax & 0xFFFF0000u) | h;
+      } else if (key > (rmax & 0xFFFFu)) {
+        rmax = (rmax & 0xFFFF0000u) | key;
+      }
+      abt |= 1u << j;
+      mo = key > mo ? key : mo;
+    }
+    if (kMode == 3) lse_fold_block_max<false, 1, 8>(st, xt, vec_max<8>(xt[0]));
+    if (mo != 0u && mo >= th_o && (!cap_signed || (int)(short)unord16(mo) >= th_s)) {
+      const uint32_t slot = atomicAdd(&sm.pool_n, 1u);
+      if (slot < kCap) {
+        sm.qd[slot] = u32x4{wt[0], wt[1], wt[2], wt[3]};
+        sm.qv[slot] = (uint16_t)nvec;
+      } else {
+        atomicMax(&sm.drop_ord, mo);
+      }
     }
   }
-  if (spill) atomicOr(&sm.flags, 1u);
-  {
-    const uint32_t cs = wave_sum_u32(counted);
-    if (lane == 0) atomicAdd(&sm.n_counted, cs);
-  }
-  const Lse3 rl = block_lse3<kB>(st, sm.red_f);  // (its barrier publishes the stream's LDS writes)
+  __syncthreads();  // the stream is complete
 
-  // ---- 4. row status
-  const float lse_m = rl.m, lse_ln = __builtin_amdgcn_logf(rl.s) * kLn2;
+  // ---- 5. maxima, escapes; the row status
+  sm.x.own.w[tid] = 0ull;
+  sm.x.own.c[tid] = 0u;
+  int topA = kNV, topB = kNV;  // penalty: smallest nonempty value bin of region A / P
+  uint32_t tot = 0u;           // penalty: tokens in the value bins and the spill words
+  uint32_t key = 0u;           // no penalty: ord16 key of the allowed maximum
+  if (kPen) {
+    if (tid < kOwners) {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int v = tid * kPer + rot(j);
+        const uint32_t c1 = cnt(sm, 0u, v), c2 = cnt(sm, kR2, v);
+        if (c1) topA = v < topA ? v : topA;
+        if (c2) topB = v < topB ? v : topB;
+        tot += c1 + c2;
+      }
+    } else if (kMode == 3) {
+      const int q = tid - kOwners;  // 0..15: the 64 spill words
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t s = sm.hist[kSpill + 4 * q + i];
+        tot += (s & 0xFFFFu) + (s >> 16);
+      }
+    }
+  } else if (cap_signed) {
+    const int lo = (int)(short)(rmax & 0xFFFFu), hi = (int)(short)(rmax >> 16);
+    const int mv = lo > hi ? lo : hi;
+    key = mv >= 0 ? ((uint32_t)mv | 0x8000u) : 0u;  // (the maximum is >= theta >= 0)
+  } else {
+    key = (rmax & 0xFFFFu) > (rmax >> 16) ? (rmax & 0xFFFFu) : (rmax >> 16);
+  }
+  Lse3 rl{kNegInf, 0.0f, 0.0f};
+  if (kMode == 3) rl = block_lse3<kB>(st, sm.red_f);
+  {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const int oa = __shfl_xor(topA, o, kWave), ob = __shfl_xor(topB, o, kWave);
+      const uint32_t ok = (uint32_t)__shfl_xor((int)key, o, kWave);
+      topA = oa < topA ? oa : topA;
+      topB = ob < topB ? ob : topB;
+      key = ok > key ? ok : key;
+    }
+    tot = wave_sum_u32(tot);
+    __syncthreads();
+    if (lane == 0) {
+      sm.red_u[wid][0] = (uint32_t)topA;
+      sm.red_u[wid][1] = (uint32_t)topB;
+      sm.red_u[wid][2] = tot;
+      sm.red_u[wid][3] = key;
+    }
+    __syncthreads();
+    topA = topB = kNV;
+    tot = key = 0u;
+#pragma unroll
+    for (int i = 0; i < kW; ++i) {
+      topA = (int)sm.red_u[i][0] < topA ? (int)sm.red_u[i][0] : topA;
+      topB = (int)sm.red_u[i][1] < topB ? (int)sm.red_u[i][1] : topB;
+      tot += sm.red_u[i][2];
+      key = sm.red_u[i][3] > key ? sm.red_u[i][3] : key;
+    }
+  }
+  // escapes (values above the bins, infinities, NaN) and 16-bit count
+  // overflows (the counts then miss tokens) go to the row-wise path
+  {
+    const uint32_t e1 = sm.hist[kNI], e2 = kMode ? sm.hist[kR2 + kNI] : 0u;
+    if ((e1 | e2) != 0u) return false;
+  }
+  if (kPen && tot != (uint32_t)V) return false;
+  if (!kPen && key != 0u) topA = vb_of(unord16(key));
   int32_t status = GTP_ROW_OK;
-  if (rl.s != rl.s || rl.m == kPosInf) status = GTP_ROW_NONFINITE;
+  if (kMode == 3 && (rl.s != rl.s || rl.m == kPosInf)) status = GTP_ROW_NONFINITE;
   else if (sm.flags & 2u) status = GTP_ROW_BAD_HISTORY;
   else if (!(u >= 0.0f && u < 1.0f)) status = GTP_ROW_BAD_UNIFORM;
   if (status != GTP_ROW_OK) {
     if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
     return true;
   }
-  if (sm.flags & 1u) return false;
-
-  // ---- 5. m, weights and the block scan
-  const int hi = kBins - 1 - kPer * tid, lo = hi - (kPer - 1);
-  uint32_t cu[kPer / 2], cp[kPer / 2];
-#pragma unroll
-  for (int i = 0; i < kPer / 2; ++i) {
-    cu[i] = sm.cnt[(lo >> 1) + i];
-    cp[i] = sm.pcnt[(lo >> 1) + i];
+  float m = kNegInf;
+  if (topA >= 0 && topA < kNV) m = r.ybin(topA);
+  if (kPen && topB < kNV) {
+    const float yp = r.ypen(topB);
+    if (!(yp < kPosInf)) return false;  // the penalty overflowed: hand over
+    m = yp > m ? yp : m;
   }
-  // count of bin hi - i
-  auto cnt_u = [&](int i) -> uint32_t { return (cu[kPer / 2 - 1 - (i >> 1)] >> ((i & 1) ? 0 : 16)) & 0xFFFFu; };
-  auto cnt_p = [&](int i) -> uint32_t { return (cp[kPer / 2 - 1 - (i >> 1)] >> ((i & 1) ? 0 : 16)) & 0xFFFFu; };
-  uint32_t mk = 0u;  // ord32 key of the largest processed logit (0: none)
-  bool bad_y = false;
-#pragma unroll
-  for (int i = kPer - 1; i >= 0; --i) {
-    if (cnt_u(i)) mk = ord32(r.ybin(hi - i));
-  }
-  {
-    float yp = kNegInf;
-    bool any = false;
-#pragma unroll
-    for (int i = kPer - 1; i >= 0; --i) {
-      if (cnt_p(i)) {
-        yp = r.ypen(hi - i);
-        any = true;
-      }
-    }
-    if (any) {
-      if (!(yp > kNegInf && yp < kPosInf)) bad_y = true;
-      else mk = ord32(yp) > mk ? ord32(yp) : mk;
-    }
-  }
-  const int zero_owner = (kBins - 1 - kBins / 2) / kPer;
-  const uint32_t zt = sm.zc + sm.pz;
-  if (tid == zero_owner && zt) mk = ord32(0.0f) > mk ? ord32(0.0f) : mk;
-  if (bad_y) atomicOr(&sm.flags, 1u);
-  mk = block_max_u32(sm, mk);
-  if (sm.flags & 1u) return false;
-  if (mk == 0u) {
+  if (m == kNegInf) {
     if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
     return true;
   }
-  const float m = unord32(mk);
-  unsigned long long Wt = 0ull;
-  uint32_t Nt = 0u;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const uint32_t c = cnt_u(i);
-    if (c) {
-      Wt += (unsigned long long)c * detexp_fix(r.ybin(hi - i) - m);
-      Nt += c;
+  // The zero bins hold zeros and values below 2^-40 as the value 0: exact
+  // when every such token weighs what a zero weighs (DETEXP_FIX is monotone:
+  // the extremes decide) and the maximum is not among them.
+  if (m == 0.0f) return false;
+  if ((sm.hist[0] | (kPen ? sm.hist[kR2] : 0u)) != 0u) {
+    const float xt = u2f((kBase - 1u) << 16);  // the largest magnitude below the bins
+    float hi = r.y_of(xt), lo = r.y_of(-xt);
+    if (kPen) {
+      const float y3 = r.y_of(r.pen_v(xt)), y4 = r.y_of(r.pen_v(-xt));
+      hi = y3 > hi ? y3 : hi;
+      lo = y4 < lo ? y4 : lo;
     }
+    if (!(hi < m) || detexp_fix(hi - m) != detexp_fix(lo - m)) return false;
   }
-  // penalised raw bins whose y lies in this thread's range: ceil_bin(ypen(p))
-  // in [lo, hi], i.e. ybin(lo - 1) < ypen(p) <= ybin(hi); ypen grows with p
-  int pl = 0, ph = -1;
-  if (r.use_pen) {
-    const float ylo = lo > 0 ? r.ybin(lo - 1) : kNegInf, yhi = r.ybin(hi);
-    int a0 = 0, a1 = kBins;  // first p with ypen(p) > ylo
-    while (a0 < a1) {
-      const int mid = (a0 + a1) >> 1;
-      if (r.ypen(mid) > ylo) a1 = mid;
-      else a0 = mid + 1;
+
+  // ---- 6. weights, the penalised values' owners, the block scan
+  // The per-value work is spread over all waves: in layer j, lane l of wave w
+  // takes value bin 1024 j + 64 w + l, and the 16 lanes of a DPP row (one
+  // owning thread's range) sum into own.w / own.c of that thread; penalised
+  // values add to the thread whose bins hold their y.  Without the per-token
+  // fold the raw log-sum-exp is folded here from the counts (online).
+  float lm = kNegInf, lsum = 0.0f;
+  uint32_t n2 = 0u;  // region-2 tokens (no penalty: the masked tokens)
+  bool unowned = false;
+  auto lse_add = [&](float x, uint32_t c) {
+    if (x > lm) {
+      lsum = lsum * __builtin_amdgcn_exp2f((lm - x) * kLog2e) + (float)c;
+      lm = x;
+    } else {
+      lsum += (float)c * __builtin_amdgcn_exp2f((x - lm) * kLog2e);
     }
-    int b0 = 0, b1 = kBins;  // first p with ypen(p) > yhi
-    while (b0 < b1) {
-      const int mid = (b0 + b1) >> 1;
-      if (r.ypen(mid) > yhi) b1 = mid;
-      else b0 = mid + 1;
+  };
+  for (int j = 0; j < kPer; ++j) {
+    const int v = 1024 * j + kWave * wid + lane;
+    const bool in = v < kNV;
+    const uint32_t c = in ? cnt(sm, 0u, v) : 0u;
+    const uint32_t c2 = (kMode != 0 && in) ? cnt(sm, kR2, v) : 0u;
+    if (!__ballot((c | c2) != 0u)) continue;
+    unsigned long long wv = 0ull;
+    if (c) {
+      wv = (unsigned long long)c * detexp_fix(r.ybin(v) - m);
+      if (kMode != 3) lse_add(vb_x(v), c);
     }
-    pl = a0;
-    ph = b0 - 1;
-    for (int p = pl; p <= ph; ++p) {
-      const uint32_t c = count16(sm.pcnt, p);
-      if (c) {
-        Wt += (unsigned long long)c * detexp_fix(r.ypen(p) - m);
-        Nt += c;
+    if (kMode != 0 && c2) {
+      if (kMode != 3) lse_add(vb_x(v), c2);
+      if (!kPen) n2 += c2;
+      if (kPen) {
+        const float y = r.ypen(v);
+        const int g = ceil_v(r, y);
+        if (g < 0) {
+          unowned = true;
+        } else {
+          atomicAdd(&sm.x.own.w[g / kPer], (unsigned long long)c2 * detexp_fix(y - m));
+          atomicAdd(&sm.x.own.c[g / kPer], c2);
+        }
       }
     }
+    const unsigned long long rw = row_scan_u64(wv);
+    const uint32_t rc = row_scan_u32(c);
+    if ((lane & 15) == 15 && rc != 0u) {
+      atomicAdd(&sm.x.own.w[v >> 4], rw);
+      atomicAdd(&sm.x.own.c[v >> 4], rc);
+    }
   }
-  if (tid == zero_owner && zt) {
-    Wt += (unsigned long long)zt * detexp_fix(0.0f - m);
-    Nt += zt;
-  }
-  unsigned long long ew, W;
-  uint32_t ec, N;
-  block_scan2(sm, Wt, Nt, ew, ec, W, N);
-  // every counted token has an owner (no count overflowed 16 bits, no
-  // penalised value above the bins)
-  if (N != sm.n_counted + zt) return false;
-
-  // ---- 6. the cut: the thread whose range holds floor(P W)
-  const unsigned long long F = floor_mul(a.P, W);
-  if (ew <= F && F < ew + Wt) {
-    sm.owner[0] = tid;
-    sm.o_ew[0] = ew;
-    sm.o_ec[0] = ec;
-    sm.o_pl[0] = pl;
-    sm.o_ph[0] = ph;
-  }
+  if (kPen && unowned) atomicOr(&sm.flags, 1u);
   __syncthreads();
+  if (kPen && (sm.flags & 1u)) return false;
+  const unsigned long long Wt = sm.x.own.w[tid];
+  const uint32_t Nt = sm.x.own.c[tid];
+  // block scan of (Wt, Nt) in thread order, with the sums of n2 and the
+  // (lm, lsum) merge
+  unsigned long long ew, W;
+  uint32_t ec, N, N2;
+  float lse_m, lse_s;
+  {
+    const unsigned long long iw = wave_scan_u64(Wt);
+    const uint32_t ic = wave_scan_u32(Nt);
+    const uint32_t s2 = wave_sum_u32(n2);
+    if (kMode != 3) wave_lse2(lm, lsum);
+    __syncthreads();  // (own is read)
+    if (lane == kWave - 1) {
+      sm.red_w[wid] = iw;
+      sm.red_u[wid][0] = ic;
+      sm.red_u[wid][1] = s2;
+      sm.red_f[wid][0] = lm;
+      sm.red_f[wid][1] = lsum;
+    }
+    __syncthreads();
+    unsigned long long bw = 0ull;
+    uint32_t bc = 0u;
+    W = 0ull;
+    N = N2 = 0u;
+    lse_m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < kW; ++i) {
+      const unsigned long long vw = sm.red_w[i];
+      const uint32_t vc = sm.red_u[i][0];
+      if (i < wid) {
+        bw += vw;
+        bc += vc;
+      }
+      W += vw;
+      N += vc;
+      N2 += sm.red_u[i][1];
+      lse_m = sm.red_f[i][0] > lse_m ? sm.red_f[i][0] : lse_m;
+    }
+    lse_s = 0.0f;
+    if (kMode != 3) {
+#pragma unroll
+      for (int i = 0; i < kW; ++i)
+        if (sm.red_f[i][1] > 0.0f)
+          lse_s += sm.red_f[i][1] * __builtin_amdgcn_exp2f((sm.red_f[i][0] - lse_m) * kLog2e);
+    }
+    ew = bw + iw - Wt;
+    ec = bc + ic - Nt;
+  }
+  // no penalty: every token is in a value bin (the counts add up)
+  if (!kPen && N + N2 != (uint32_t)V) return false;
+  sm.x.ex.w[tid] = ew;
+  sm.x.ex.c[tid] = ec;
+  if (tid == 0) {
+    sm.x.ex.w[kB] = W;
+    sm.x.ex.c[kB] = N;
+  }
+  if (kMode == 3) {
+    lse_m = rl.m;
+    lse_s = rl.s;
+  }
+  const float lse_ln = __builtin_amdgcn_logf(lse_s) * kLn2;
+  __syncthreads();
+
+  // ---- 7. the cut and the draw (wave 0)
   if (wid == 0) {
-    Level L;
-    const bool ok = sm.owner[0] >= 0 &&
-                    resolve_range<kMask>(sm, r, sm.owner[0], m, F, sm.o_ew[0], sm.o_ec[0],
-                                         sm.o_pl[0], sm.o_ph[0], L);
+    Level L0, L1;
+    const unsigned long long F = floor_mul(a.P, W);
+    bool ok = resolve<kMode>(sm, r, m, F, L0);
+    if (ok) {
+      const unsigned long long Wp = L0.s_before + (unsigned long long)(L0.k + 1u) * L0.w;
+      ok = resolve<kMode>(sm, r, m, floor_mul(u, Wp), L1);
+    }
     if (lane == 0) {
-      sm.lv[0] = L;
-      sm.bad = ok && !(L.pbin >= 0 && L.zero_p) ? 0 : 1;
+      sm.lv[0] = L0;
+      sm.lv[1] = L1;
+      sm.bad = ok ? 0 : 1;
     }
   }
   __syncthreads();
   if (sm.bad) return false;
-  const Level L0 = sm.lv[0];
+  const Level L0 = sm.lv[0], L1 = sm.lv[1];
   const uint32_t R = L0.n_before + L0.k + 1u;
   const unsigned long long Wp = L0.s_before + (unsigned long long)(L0.k + 1u) * L0.w;
 
-  // ---- 7. the draw: floor(u W') among the kept tokens
-  const unsigned long long U = floor_mul(u, Wp);
-  if (ew <= U && U < ew + Wt) {
-    sm.owner[1] = tid;
-    sm.o_ew[1] = ew;
-    sm.o_ec[1] = ec;
-    sm.o_pl[1] = pl;
-    sm.o_ph[1] = ph;
-  }
-  __syncthreads();
-  if (wid == 0) {
-    Level L;
-    const bool ok = sm.owner[1] >= 0 &&
-                    resolve_range<kMask>(sm, r, sm.owner[1], m, U, sm.o_ew[1], sm.o_ec[1],
-                                         sm.o_pl[1], sm.o_ph[1], L);
-    if (lane == 0) {
-      sm.lv[1] = L;
-      sm.bad = ok && !(L.pbin >= 0 && L.zero_p) ? 0 : 1;
-    }
-  }
-  __syncthreads();
-  if (sm.bad) return false;
-  const Level L1 = sm.lv[1];
-
   // ---- 8. ids: from the pool when it holds both values, else a rescan
-  if (level_in_pool<kMask>(sm, r, L0, theta) && level_in_pool<kMask>(sm, r, L1, theta)) {
-    uint32_t* bm0 = sm.cnt;   // id bitmaps of the two levels (the counts are no longer needed)
-    uint32_t* bm1 = sm.pcnt;
-    for (int i = tid; i < kBins / 2; i += kB) {
-      bm0[i] = 0u;
-      bm1[i] = 0u;
-    }
+  const uint32_t th = sm.theta, drop = sm.drop_ord;
+  const uint32_t th_ord = th == kNone ? 0u : ord16(th);
+  auto pooled = [&](uint32_t h) { return h == kNone || (ord16(h) >= th_ord && ord16(h) > drop); };
+  if (pooled(L0.hu) && pooled(L0.hp) && pooled(L1.hu) && pooled(L1.hp)) {
+    const bool big0 = L0.n > (uint32_t)kSmall, big1 = L1.n > (uint32_t)kSmall;
+    const int nwords = (int)((V + 31) / 32);
+    // level l: a list at hist[l * 8192] (small) or an id bitmap there (big)
+    if (big0)
+      for (int i = tid; i < nwords; i += kB) sm.hist[i] = 0u;
+    if (big1)
+      for (int i = tid; i < nwords; i += kB) sm.hist[8192 + i] = 0u;
     __syncthreads();
-    const uint32_t np = sm.pool_n < (uint32_t)kPool ? sm.pool_n : (uint32_t)kPool;
-    for (uint32_t s2 = tid; s2 < np; s2 += kB) {
-      const uint32_t q = sm.qid[s2], h = sm.qh[s2];
-      const uint32_t id = q & 0x7FFFFFFFu;
-      const bool pn = q >> 31;
-      if (level_has(L0, pn, h)) atomicOr(&bm0[id >> 5], 1u << (id & 31));
-      if (level_has(L1, pn, h)) atomicOr(&bm1[id >> 5], 1u << (id & 31));
-    }
-    __syncthreads();
-    // thread t: words 8t .. 8t + 7 of each bitmap
-    uint32_t w0[8], w1[8], p0 = 0u, p1 = 0u;
+
+    auto add = [&](int l, bool big, uint32_t id) {
+      uint32_t* base = sm.hist + l * 8192;
+      if (big) {
+        atomicOr(&base[id >> 5], 1u << (id & 31));
+      } else {
+        const uint32_t s = atomicAdd(&sm.list_n[l], 1u);
+        if (s < (uint32_t)kSmall) base[s] = id;
+      }
+    };
+    const uint32_t np = sm.pool_n < kCap ? sm.pool_n : kCap;
+    for (uint32_t s = tid; s < np; s += kB) {
+      const u32x4 q = sm.qd[s];
+      const uint32_t vi = sm.qv[s];
+      const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+      const uint32_t ab = kMask ? (r.mask[vi >> 2] >> ((vi & 3) * 8)) & 0xFFu : 0xFFu;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      w0[i] = bm0[8 * tid + i];
-      w1[i] = bm1[8 * tid + i];
-      p0 += __builtin_popcount(w0[i]);
-      p1 += __builtin_popcount(w1[i]);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t id = vi * 8u + (uint32_t)j;
+        if (!((ab >> j) & 1u) || id >= (uint32_t)V) continue;
+        const uint32_t h = (j & 1) ? wd[j >> 1] >> 16 : wd[j >> 1] & 0xFFFFu;
+        const bool pn = kPen && ((sm.pen()[id >> 5] >> (id & 31)) & 1u);
+        if (in_level(L0, pn, h)) add(0, big0, id);
+        if (in_level(L1, pn, h)) add(1, big1, id);
+      }
     }
-    unsigned long long e0, t0;
-    uint32_t e1, t1;
-    block_scan2(sm, p0, p1, e0, e1, t0, t1);
-    if (t0 != L0.n || t1 != L1.n) return false;
-    // the k-th set bit of this thread's 8 words (unrolled: no indexed registers)
-    auto find = [&](const uint32_t(&wv)[8], uint32_t k) -> int32_t {
-      int32_t id = -1;
+    __syncthreads();
+    // small levels: wave l ranks its list
+    if (wid < 2) {
+      const Level& L = wid ? L1 : L0;
+      const bool big = wid ? big1 : big0;
+      if (!big) {
+        const uint32_t n = sm.list_n[wid];
+        const uint32_t* lst = sm.hist + wid * 8192;
+        if (n != L.n) {
+          if (lane == 0) sm.bad = 1;
+        } else {
+          // rank of each listed id among the list, in registers
+          const uint32_t my = (uint32_t)lane < n ? lst[lane] : 0xFFFFFFFFu;
+          uint32_t rank = 0u;
+#pragma unroll
+          for (int j = 0; j < kWave; ++j)
+            rank += (uint32_t)__builtin_amdgcn_readlane((int)my, j) < my ? 1u : 0u;
+          if ((uint32_t)lane < n && rank == L.k) sm.id_out[wid] = (int32_t)my;
+        }
+      }
+    }
+    // big levels: popcounts of the bitmap words, one block scan
+    if (big0 || big1) {
+      uint32_t w0[8], w1[8], p0 = 0u, p1 = 0u;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const uint32_t pc = __builtin_popcount(wv[i]);
-        if (id < 0 && k < pc) {
-          uint32_t x = wv[i];
-          for (uint32_t j = 0; j < k; ++j) x &= x - 1u;
-          id = (int32_t)((8 * tid + i) * 32 + __builtin_ctz(x));
-        }
-        k = id < 0 ? k - pc : k;
+        const int wi = 8 * tid + i;
+        w0[i] = big0 && wi < nwords ? sm.hist[wi] : 0u;
+        w1[i] = big1 && wi < nwords ? sm.hist[8192 + wi] : 0u;
+        p0 += __builtin_popcount(w0[i]);
+        p1 += __builtin_popcount(w1[i]);
       }
-      return id;
-    };
-    if (e0 <= L0.k && L0.k < e0 + p0) sm.id_out[0] = find(w0, (uint32_t)(L0.k - e0));
-    if (e1 <= L1.k && L1.k < e1 + p1) sm.id_out[1] = find(w1, L1.k - e1);
+      unsigned long long e0, t0;
+      uint32_t e1, t1;
+      float f0;
+      block_scan2(sm, p0, p1, 0.0f, e0, e1, t0, t1, f0);
+      if ((big0 && t0 != L0.n) || (big1 && t1 != L1.n)) return false;
+      auto find = [&](const uint32_t(&wv)[8], uint32_t k) -> int32_t {
+        int32_t id = -1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t pc = __builtin_popcount(wv[i]);
+          if (id < 0 && k < pc) {
+            uint32_t x = wv[i];
+            for (uint32_t j = 0; j < k; ++j) x &= x - 1u;
+            id = (int32_t)((8 * tid + i) * 32 + __builtin_ctz(x));
+          }
+          k = id < 0 ? k - pc : k;
+        }
+        return id;
+      };
+      if (big0 && e0 <= L0.k && L0.k < e0 + p0) sm.id_out[0] = find(w0, (uint32_t)(L0.k - e0));
+      if (big1 && e1 <= L1.k && L1.k < e1 + p1) sm.id_out[1] = find(w1, L1.k - e1);
+    }
     __syncthreads();
+    if (sm.bad) return false;
   } else {
-    rescan_ids<kMask>(sm, r);
+    rescan_ids<kMode>(sm, r);
   }
 
-  // ---- 9. outputs
+  // ---- 9. outputs (both ids found, or the row goes to the row-wise path)
+  if (sm.id_out[0] < 0 || sm.id_out[1] < 0) return false;
   if (tid == 0) {
     const int32_t id_thr = sm.id_out[0], id_draw = sm.id_out[1];
-    const bool dp = r.use_pen && ((sm.pen[id_draw >> 5] >> (id_draw & 31)) & 1u);
-    const int32_t bn = dp ? L1.pbin : L1.ubin;
-    const float x_draw = bn >= 0 ? bin_x(bn) : 0.0f;
+    const bool dp = kPen && ((sm.pen()[id_draw >> 5] >> (id_draw & 31)) & 1u);
+    const uint32_t hd = dp ? L1.hp : L1.hu;
+    const float x_draw = u2f(hd << 16);
     const float slp = __builtin_amdgcn_logf((float)((double)L1.w / (double)Wp)) * kLn2;
     write_row(a, b, GTP_ROW_OK, id_draw, raw_logprob(x_draw, lse_m, lse_ln), slp, (int32_t)R,
               L0.y, id_thr);
@@ -911,14 +1228,15 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
 // One row per workgroup.  A row outside the top-p path's bounds is handed
 // over: its index goes to handover[1 + n] with n = handover[0]++, and
 // sampler_handover_kernel, launched right after on the same stream, runs the
-// row-wise path for the listed rows and returns handover[0] to zero.  The
+// row-wise path for the listed rows and returns the list to zero.  The
 // row-wise path's registers thus never weigh on this kernel.
-template <bool kMask>
+// kMode bit 0: repetition penalty active; bit 1: allow mask.
+template <int kMode>
 __global__ __launch_bounds__(topp::kB) void sampler_topp_kernel(SamplerArgs a,
                                                                 uint32_t* __restrict__ handover) {
   __shared__ topp::Smem sm;
   const int64_t b = blockIdx.x;
-  if (!topp::topp_row<kMask>(a, b, sm) && threadIdx.x == 0)
+  if (!topp::topp_row<kMode>(a, b, sm) && threadIdx.x == 0)
     handover[1 + atomicAdd(handover, 1u)] = (uint32_t)b;
 }
 
