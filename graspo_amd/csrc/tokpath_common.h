@@ -81,7 +81,11 @@ __device__ __forceinline__ float rank_key_y(uint64_t k) { return unord32((uint32
 
 // ------------------------------------------------------------ DETEXP_FIX
 // round(e^d * 2^40) for d <= 0; the step list is the contract written out in
-// include/graspo_tokpath.h and must not be reordered.
+// include/graspo_tokpath.h and must not be reordered.  The final scaling by
+// 2^s is branch-free: s >= 0 shifts left; s < 0 rounds half to even as
+// (mant + 2^(sh-1) - 1 + lsb) >> sh with sh = -s clamped to [1, 26] (every
+// sh >= 25 gives 0 for a 24-bit mant).  Equal to the plain two-branch form
+// for every fp32 d <= 0 (checked over all of them).
 __device__ __forceinline__ uint64_t detexp_fix(float d) {
   if (!(d >= -30.0f)) return 0ull;
   float n = __builtin_rintf(d * 0x1.715476p+0f);
@@ -95,18 +99,13 @@ __device__ __forceinline__ uint64_t detexp_fix(float d) {
   p = __builtin_fmaf(p, r, 0x1p-1f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  uint32_t pb = f2u(p);
-  uint64_t mant = (uint64_t)((pb & 0x7FFFFFu) | 0x800000u);
-  int e = (int)((pb >> 23) & 0xFFu) - 150;
-  int s = e + 40 + (int)n;
-  if (s >= 0) return mant << s;
+  const uint32_t pb = f2u(p);
+  const uint32_t mant = (pb & 0x7FFFFFu) | 0x800000u;
+  const int s = (int)((pb >> 23) & 0xFFu) - 150 + 40 + (int)n;
   int sh = -s;
-  if (sh > 25) return 0ull;
-  uint64_t q = mant >> sh;
-  uint64_t rem = mant & ((1ull << sh) - 1ull);
-  uint64_t half = 1ull << (sh - 1);
-  if (rem > half || (rem == half && (q & 1ull))) q += 1ull;
-  return q;
+  sh = sh < 1 ? 1 : (sh > 26 ? 26 : sh);
+  const uint32_t q = (mant + ((1u << (sh - 1)) - 1u) + ((mant >> sh) & 1u)) >> sh;
+  return s >= 0 ? (uint64_t)mant << s : (uint64_t)q;
 }
 
 // log_softmax(x)_i = x_i - m - ln s evaluated in fp64 and rounded once:

@@ -280,9 +280,10 @@ __device__ __forceinline__ void for_each_valid(const Row<T>& r, const SamplerSme
 }
 
 // Write the outputs of a row.
-__device__ __forceinline__ void write_row(const SamplerArgs& a, int64_t b, int32_t status, int64_t id,
-                                          float lp, float slp, int32_t kept, float tv, int32_t tid) {
-  const bool fin = a.finished && a.finished[b];
+// (`fin`: the row's finished flag, read by the caller)
+__device__ __forceinline__ void write_row_f(const SamplerArgs& a, int64_t b, bool fin, int32_t status,
+                                            int64_t id, float lp, float slp, int32_t kept, float tv,
+                                            int32_t tid) {
   if (status != GTP_ROW_OK) {
     a.out_ids[b] = fin ? a.pad_id : -1;
     if (a.out_lp) a.out_lp[b] = __builtin_nanf("");
@@ -299,6 +300,10 @@ __device__ __forceinline__ void write_row(const SamplerArgs& a, int64_t b, int32
     if (a.out_tid) a.out_tid[b] = tid;
   }
   if (a.out_status) a.out_status[b] = status;
+}
+__device__ __forceinline__ void write_row(const SamplerArgs& a, int64_t b, int32_t status, int64_t id,
+                                          float lp, float slp, int32_t kept, float tv, int32_t tid) {
+  write_row_f(a, b, a.finished && a.finished[b], status, id, lp, slp, kept, tv, tid);
 }
 
 // ------------------------------------------------------ radix descent path

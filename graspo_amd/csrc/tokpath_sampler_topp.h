@@ -100,7 +100,7 @@ struct alignas(16) Smem {
   // pool: captured vectors; with a penalty, entries [kPoolVPen, kPoolV)
   // hold the bitmap of penalised ids (GTP_SAMPLER_MAX_V bits)
   u32x4 qd[kPoolV];
-  uint16_t qv[kPoolV];  // ... their vector index
+  uint32_t qv[kPoolV];  // ... their vector index | allow byte << 16
   union {
     struct {
       unsigned long long w[kB];  // penalised values' weight per owning thread
@@ -117,11 +117,14 @@ struct alignas(16) Smem {
   Level lv[2];  // the cut (0) and the drawn (1) value
   int32_t id_out[2];
   uint32_t scan_n[kW][2];
-  uint32_t pool_n;
+  uint32_t seg_n[kW];  // pool entries of each wave's own segment
+  uint32_t over_n;     // entries of the shared overflow area
   uint32_t list_n[2];
   uint32_t chunk_ctr;
   uint32_t drop_ord;  // largest ord16 key of a vector the full pool dropped, 0: none
   uint32_t theta;     // bf16 bits of theta, kNone: every allowed token is captured
+  float u;            // the row's uniform and finished flag (read at the start)
+  uint32_t fin;
   uint32_t flags;     // bit 0: hand over; bit 1: bad history id
   int32_t bad;
   __device__ __forceinline__ uint32_t* pen() { return reinterpret_cast<uint32_t*>(&qd[kPoolVPen]); }
@@ -563,7 +566,6 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
   r.nvec = a.V / 8;
   r.rho = a.rho;
   r.Tc = a.T > 1e-6f ? a.T : 1e-6f;
-  const float u = a.uniforms[b];
   const int64_t V = a.V, nvec = r.nvec;
   const uint32_t nchunks = (uint32_t)((nvec + kChunk - 1) / kChunk);
   const uint32_t per = nchunks / kW;
@@ -604,8 +606,12 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
       for (int64_t i = tid; i < (V + 127) / 128; i += kB) reinterpret_cast<u32x4*>(sm.pen())[i] = z;
   }
   if (tid == 0) {
+    // (read now: a global load after the stream waits behind the other
+    // rows' traffic)
+    sm.u = a.uniforms[b];
+    sm.fin = a.finished && a.finished[b];
     sm.chunk_ctr = 2u * kW;
-    sm.pool_n = 0u;
+    sm.over_n = 0u;
     sm.drop_ord = 0u;
     sm.theta = kNone;
     sm.flags = 0u;
@@ -653,21 +659,34 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
   int th_s = 0;           // theta as a signed 16-bit pattern
   uint32_t th_o = 1u;     // ord16(theta) (1: every allowed token)
   uint32_t rmax = 0u;     // running maximum of the allowed tokens (packed, test's domain)
+  // pool layout: 16 wave segments of kSegV entries, then a shared overflow
+  // area of kOver entries
   constexpr uint32_t kCap = kPen ? kPoolVPen : kPoolV;
-  // a vector whose test passed goes whole into the pool (one LDS atomic per
-  // wave and step); a full pool keeps the largest key it dropped
+  constexpr uint32_t kSegV = kPen ? 64u : 160u;
+  constexpr uint32_t kOver = kCap - kW * kSegV;
+  uint32_t seg = 0u;  // this wave's pool entries so far (wave-uniform)
+  // a vector whose test passed goes whole into this wave's pool segment (no
+  // LDS round trip); past its end, into the overflow area (one LDS atomic
+  // per wave and step); a full pool keeps the largest key it dropped
   auto append = [&](bool c, uint32_t vi, const u32x4& vec, uint32_t ab) __attribute__((always_inline)) {
     const unsigned long long bal = __ballot(c);
     if (!bal) return;
-    uint32_t base = 0u;
-    if (lane == 0) base = atomicAdd(&sm.pool_n, (uint32_t)__builtin_popcountll(bal));
-    base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+    const uint32_t base = seg, n = (uint32_t)__builtin_popcountll(bal);
+    seg += n;
+    const uint32_t first_over = base > kSegV ? base : kSegV;  // segment slot of the first overflow
+    uint32_t obase = 0u;
+    if (base + n > kSegV) {
+      if (lane == 0) obase = atomicAdd(&sm.over_n, base + n - first_over);
+      obase = (uint32_t)__builtin_amdgcn_readlane((int)obase, 0);
+    }
     if (c) {
       const uint32_t slot = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-      if (slot < kCap) {
-        sm.qd[slot] = vec;
-        sm.qv[slot] = (uint16_t)vi;
+      const uint32_t o = obase + (slot - first_over);  // (used when slot >= kSegV)
+      if (slot < kSegV || o < kOver) {
+        const uint32_t e = slot < kSegV ? wid * kSegV + slot : kW * kSegV + o;
+        sm.qd[e] = vec;
+        sm.qv[e] = vi | (ab << 16);
       } else {
         const uint32_t wd[4] = {vec.x, vec.y, vec.z, vec.w};
         uint32_t mo = 0u;
@@ -859,15 +878,18 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     }
     if (kMode == 3) lse_fold_block_max<false, 1, 8>(st, xt, vec_max<8>(xt[0]));
     if (mo != 0u && mo >= th_o && (!cap_signed || (int)(short)unord16(mo) >= th_s)) {
-      const uint32_t slot = atomicAdd(&sm.pool_n, 1u);
-      if (slot < kCap) {
-        sm.qd[slot] = u32x4{wt[0], wt[1], wt[2], wt[3]};
-        sm.qv[slot] = (uint16_t)nvec;
+      const uint32_t o = seg < kSegV ? 0u : atomicAdd(&sm.over_n, 1u);
+      if (seg < kSegV || o < kOver) {  // (wave 0's segment, else the overflow area)
+        const uint32_t e = seg < kSegV ? seg : kW * kSegV + o;
+        sm.qd[e] = u32x4{wt[0], wt[1], wt[2], wt[3]};
+        sm.qv[e] = (uint32_t)nvec | (abt << 16);
       } else {
         atomicMax(&sm.drop_ord, mo);
       }
+      ++seg;
     }
   }
+  if (lane == 0) sm.seg_n[wid] = seg < kSegV ? seg : kSegV;
   __syncthreads();  // the stream is complete
 
   // ---- 5. maxima, escapes; the row status
@@ -939,12 +961,13 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
   }
   if (kPen && tot != (uint32_t)V) return false;
   if (!kPen && key != 0u) topA = vb_of(unord16(key));
+  const float u = sm.u;
   int32_t status = GTP_ROW_OK;
   if (kMode == 3 && (rl.s != rl.s || rl.m == kPosInf)) status = GTP_ROW_NONFINITE;
   else if (sm.flags & 2u) status = GTP_ROW_BAD_HISTORY;
   else if (!(u >= 0.0f && u < 1.0f)) status = GTP_ROW_BAD_UNIFORM;
   if (status != GTP_ROW_OK) {
-    if (tid == 0) write_row(a, b, status, -1, 0.f, 0.f, 0, 0.f, -1);
+    if (tid == 0) write_row_f(a, b, sm.fin != 0u, status, -1, 0.f, 0.f, 0, 0.f, -1);
     return true;
   }
   float m = kNegInf;
@@ -955,7 +978,7 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     m = yp > m ? yp : m;
   }
   if (m == kNegInf) {
-    if (tid == 0) write_row(a, b, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
+    if (tid == 0) write_row_f(a, b, sm.fin != 0u, GTP_ROW_EMPTY, -1, 0.f, 0.f, 0, 0.f, -1);
     return true;
   }
   // The zero bins hold zeros and values below 2^-40 as the value 0: exact
@@ -975,15 +998,22 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
 
   // ---- 6. weights, the penalised values' owners, the block scan
   // The per-value work is spread over all waves: in layer j, lane l of wave w
-  // takes value bin 1024 j + 64 w + l, and the 16 lanes of a DPP row (one
-  // owning thread's range) sum into own.w / own.c of that thread; penalised
+  // takes value bin 1024 j + 64 w + l and adds its weight and count to
+  // own.w / own.c of the thread that owns the bin (v / 16); penalised
   // values add to the thread whose bins hold their y.  Without the per-token
-  // fold the raw log-sum-exp is folded here from the counts (online).
+  // fold the raw log-sum-exp comes from the counts: around the known raw
+  // maximum without a mask, online with one (the masked maximum is unknown).
   float lm = kNegInf, lsum = 0.0f;
+  if (kMode == 0 || kMode == 1) {
+    lm = topA < kNV ? vb_x(topA) : kNegInf;
+    if (kMode == 1 && topB < kNV) lm = vb_x(topB) > lm ? vb_x(topB) : lm;
+  }
   uint32_t n2 = 0u;  // region-2 tokens (no penalty: the masked tokens)
   bool unowned = false;
   auto lse_add = [&](float x, uint32_t c) {
-    if (x > lm) {
+    if (kMode != 2) {
+      lsum += (float)c * __builtin_amdgcn_exp2f((x - lm) * kLog2e);
+    } else if (x > lm) {
       lsum = lsum * __builtin_amdgcn_exp2f((lm - x) * kLog2e) + (float)c;
       lm = x;
     } else {
@@ -1015,11 +1045,9 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
         }
       }
     }
-    const unsigned long long rw = row_scan_u64(wv);
-    const uint32_t rc = row_scan_u32(c);
-    if ((lane & 15) == 15 && rc != 0u) {
-      atomicAdd(&sm.x.own.w[v >> 4], rw);
-      atomicAdd(&sm.x.own.c[v >> 4], rc);
+    if (c) {  // (LDS atomics: the 16 lanes of one range meet at one address)
+      atomicAdd(&sm.x.own.w[v >> 4], wv);
+      atomicAdd(&sm.x.own.c[v >> 4], c);
     }
   }
   if (kPen && unowned) atomicOr(&sm.flags, 1u);
@@ -1036,7 +1064,8 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     const unsigned long long iw = wave_scan_u64(Wt);
     const uint32_t ic = wave_scan_u32(Nt);
     const uint32_t s2 = wave_sum_u32(n2);
-    if (kMode != 3) wave_lse2(lm, lsum);
+    if (kMode == 2) wave_lse2(lm, lsum);
+    else if (kMode != 3) lsum = wave_sum_f(lsum);
     __syncthreads();  // (own is read)
     if (lane == kWave - 1) {
       sm.red_w[wid] = iw;
@@ -1065,11 +1094,14 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
       lse_m = sm.red_f[i][0] > lse_m ? sm.red_f[i][0] : lse_m;
     }
     lse_s = 0.0f;
-    if (kMode != 3) {
+    if (kMode == 2) {
 #pragma unroll
       for (int i = 0; i < kW; ++i)
         if (sm.red_f[i][1] > 0.0f)
           lse_s += sm.red_f[i][1] * __builtin_amdgcn_exp2f((sm.red_f[i][0] - lse_m) * kLog2e);
+    } else if (kMode != 3) {
+#pragma unroll
+      for (int i = 0; i < kW; ++i) lse_s += sm.red_f[i][1];
     }
     ew = bw + iw - Wt;
     ec = bc + ic - Nt;
@@ -1122,7 +1154,7 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
       for (int i = tid; i < nwords; i += kB) sm.hist[i] = 0u;
     if (big1)
       for (int i = tid; i < nwords; i += kB) sm.hist[8192 + i] = 0u;
-    __syncthreads();
+    if (big0 || big1) __syncthreads();
 
     auto add = [&](int l, bool big, uint32_t id) {
       uint32_t* base = sm.hist + l * 8192;
@@ -1133,13 +1165,27 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
         if (s < (uint32_t)kSmall) base[s] = id;
       }
     };
-    const uint32_t np = sm.pool_n < kCap ? sm.pool_n : kCap;
-    for (uint32_t s = tid; s < np; s += kB) {
+    // the levels' values in both halves; a vector is looked at token by token
+    // only when a half equals one of them (packed compares)
+    auto pat = [](uint32_t h) { return h == kNone ? 0xFFFFFFFFu : h * 0x10001u; };
+    const uint32_t pu0 = pat(L0.hu), pp0 = pat(L0.hp), pu1 = pat(L1.hu), pp1 = pat(L1.hp);
+    auto zeq = [](uint32_t w, uint32_t pt) {
+      const uint32_t x = w ^ pt;
+      return as_u32(as_us2(x) - (us2)(unsigned short)1) & ~x & 0x80008000u;
+    };
+    const uint32_t n_over = sm.over_n < kOver ? sm.over_n : kOver;
+    for (uint32_t s = tid; s < kCap; s += kB) {
+      if (s < kW * kSegV ? s % kSegV >= sm.seg_n[s / kSegV] : s - kW * kSegV >= n_over) continue;
       const u32x4 q = sm.qd[s];
-      const uint32_t vi = sm.qv[s];
       const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-      const uint32_t ab = kMask ? (r.mask[vi >> 2] >> ((vi & 3) * 8)) & 0xFFu : 0xFFu;
+      uint32_t any = 0u;
 #pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        any |= zeq(wd[p], pu0) | zeq(wd[p], pu1);
+        if (kPen) any |= zeq(wd[p], pp0) | zeq(wd[p], pp1);
+      }
+      if (!any) continue;
+      const uint32_t vi = sm.qv[s] & 0xFFFFu, ab = sm.qv[s] >> 16;
       for (int j = 0; j < 8; ++j) {
         const uint32_t id = vi * 8u + (uint32_t)j;
         if (!((ab >> j) & 1u) || id >= (uint32_t)V) continue;
@@ -1217,7 +1263,7 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     const uint32_t hd = dp ? L1.hp : L1.hu;
     const float x_draw = u2f(hd << 16);
     const float slp = __builtin_amdgcn_logf((float)((double)L1.w / (double)Wp)) * kLn2;
-    write_row(a, b, GTP_ROW_OK, id_draw, raw_logprob(x_draw, lse_m, lse_ln), slp, (int32_t)R,
+    write_row_f(a, b, sm.fin != 0u, GTP_ROW_OK, id_draw, raw_logprob(x_draw, lse_m, lse_ln), slp, (int32_t)R,
               L0.y, id_thr);
   }
   return true;
