@@ -32,8 +32,21 @@ loop body, both on this library's sampler, with a stand-in model.
 expression, with the bf16 GEMM's TFLOP/s against the matrix-core peak.
 
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
-[64,151936] top-p only; bf16 [64,151936] masked), each timed alone with a
-512 MB buffer written between launches to evict the MALL.
+[64,151936] top-p only; bf16 [64,151936] masked; the [256,248320] rows with
+top-p only -- the decode loop's T 0.7 / P 0.9 rows, and the same with the
+history and mask -- on the top-p kernel), each timed alone with a 512 MB
+buffer written between launches to evict the MALL, and the loss-side
+logprob workload: bf16 [32768,151936] x 2 passes (policy and reference
+logits) in 4 chunks of 8192 rows each.
+
+``stream_floor_us`` is the kernel time of gtp_stream_read_rows over the
+same logits (a read-only pass with the samplers' access pattern: one
+1024-thread workgroup per row, 16-byte non-temporal loads), MALL evicted:
+the streaming floor the sampler kernels are compared with.
+
+``cpu_baseline`` times the reference's CPU path (oracle/cpu_reference.py)
+on bounded samples of every configuration, with all host threads, and names
+the host CPU.
 
 ``--calibrate-copy`` runs only a 1 GiB device-to-device copy (the reference
 kernel whose rocprof FETCH_SIZE / WRITE_SIZE scale the HBM traffic counters).
@@ -55,6 +68,51 @@ BACKWARD_KERNEL = "logprob_backward_kernel<bf16>"
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_large_vocab.md")
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_rate(fn, units: int, min_seconds: float) -> float:
+    fn()  # warmup
+    reps, t0 = 0, time.perf_counter()
+    while reps < 2 or time.perf_counter() - t0 < min_seconds:
+        fn()
+        reps += 1
+    return units * reps / (time.perf_counter() - t0)
+
+
+def cpu_baseline_configs(min_seconds: float = 3.0):
+    """The reference's CPU path on bounded samples of configurations 1-4
+    (config 5 is the headline cpu_baseline): rows/s for the samplers,
+    tokens/s for the logprob workload."""
+    from graspo_amd import workloads as W
+    from oracle import cpu_reference as CR
+
+    out = {}
+    for cfg, rows in ((1, 8), (2, 16), (3, 16)):
+        w = W.sampler_workload(cfg, device="cpu", rows=rows)
+        bits = None if w.allow_mask is None else W.unpack_mask(w.allow_mask, w.logits.shape[1])
+        kw = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p,
+                  repetition_penalty=w.repetition_penalty, history=w.history,
+                  allow_mask_bits=bits, uniforms=w.uniforms)
+        r = _cpu_rate(lambda: CR.sample_rows(w.logits, **kw), rows, min_seconds)
+        out[f"config{cfg}"] = {"value": round(r, 2), "unit": "rows/s",
+                               "sample": f"{rows} rows of {list(w.logits.shape[1:])} "
+                                         f"{str(w.logits.dtype).replace('torch.', '')}"}
+    x, t = W.logprob_workload(4, device="cpu", rows=256)
+    r = _cpu_rate(lambda: CR.logprob_entropy_rows(x, t), 256, min_seconds)
+    out["config4"] = {"value": round(r, 2), "unit": "tokens/s",
+                      "sample": "256 rows of bf16 [32768, 151936] (pass 0)"}
+    return out
 
 
 def cpu_baseline(wl_cpu, lx_cpu, lt_cpu, min_seconds: float = 10.0):
@@ -95,6 +153,8 @@ def cpu_baseline(wl_cpu, lx_cpu, lt_cpu, min_seconds: float = 10.0):
                   f"T, top-k, top-p), full V, >= {min_seconds:.0f} s; logprob: {lrows} rows of "
                   f"bf16 [8192, 248320] -> {l_tok:.1f} tokens/s",
         "logprob_tokens_per_s": round(l_tok, 2),
+        "cpu_model": cpu_model(),
+        "configs": cpu_baseline_configs(),
     }
 
 
@@ -143,8 +203,41 @@ def kernel_events(n: int):
     return evs
 
 
-def time_sampler_config(cfg: int, dev, iters: int, flush):
-    """Average kernel time of one sampler launch on workload ``cfg`` with the
+def stream_floor_us(x, flush, iters: int = 10) -> float:
+    """Average kernel time of gtp_stream_read_rows over the rows of ``x``
+    (a read-only pass with the samplers' access pattern), MALL evicted
+    before each launch: the streaming floor."""
+    import ctypes
+
+    import torch
+
+    import graspo_amd
+    from graspo_amd import ops
+
+    lib = ctypes.CDLL(graspo_amd.LIB_PATH)
+    fn = lib.gtp_stream_read_rows
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                   ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    rows, cols = x.shape
+    out = torch.zeros(rows, dtype=torch.int32, device=x.device)
+    args = (x.data_ptr(), rows, cols * x.element_size(), x.stride(0) * x.element_size(),
+            out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    for _ in range(2):
+        assert fn(*args) == 0
+    evs = kernel_events(iters)
+    for e0, e1 in evs:
+        flush.add_(1)
+        ops.time_next_launch(e0, e1)
+        assert fn(*args) == 0
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+
+
+def time_sampler_config(cfg: int, dev, iters: int, flush, kernel: str = SAMPLER_KERNEL,
+                        override: dict | None = None, drop: tuple = (), what: str | None = None):
+    """Average kernel time of one sampler launch on workload ``cfg`` (its
+    parameters changed by ``override``, inputs in ``drop`` removed) with the
     MALL evicted before every launch."""
     import torch
 
@@ -153,6 +246,9 @@ def time_sampler_config(cfg: int, dev, iters: int, flush):
 
     wl = W.sampler_workload(cfg, device=dev)
     kw = wl.kwargs()
+    for k in drop:
+        kw.pop(k, None)
+    kw.update(override or {})
     for _ in range(2):
         ops.sample(wl.logits, **kw)
     evs = kernel_events(iters)
@@ -162,13 +258,61 @@ def time_sampler_config(cfg: int, dev, iters: int, flush):
         ops.sample(wl.logits, **kw)
     torch.cuda.synchronize()
     us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
-    B = wl.logits.shape[0]
-    nbytes = wl.algorithmic_bytes()
-    return {
-        "shape": list(wl.logits.shape), "dtype": str(wl.logits.dtype).replace("torch.", ""),
+    B, V = wl.logits.shape
+    nbytes = wl.logits.numel() * wl.logits.element_size() + B * 16
+    if kw.get("allow_mask") is not None:
+        nbytes += B * ((V + 31) // 32) * 4
+    if kw.get("history") is not None:
+        nbytes += kw["history"].numel() * 4
+    floor = stream_floor_us(wl.logits, flush)
+    out = {
+        "shape": [B, V], "dtype": str(wl.logits.dtype).replace("torch.", ""), "kernel": kernel,
         "avg_us": round(us, 2), "rows_per_s": round(B / (us * 1e-6), 1),
         "algorithmic_bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
         "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "stream_floor_us": round(floor, 2),
+        "traffic": profiled_traffic(kernel + f" [{B}, {V}]"),
+    }
+    if what:
+        out["what"] = what
+    return out
+
+
+def time_logprob_config4(dev, chunk: int = 8192):
+    """The loss-side workload: bf16 [32768, 151936] logits with int32
+    targets, for the policy and the reference pass (different seeds), each
+    processed as 4 chunks of 8192 rows; every chunk launch timed through the
+    launch hook."""
+    import torch
+
+    from graspo_amd import ops
+    from graspo_amd import workloads as W
+
+    passes = [W.logprob_workload(4, device=dev, pass_index=p) for p in (0, 1)]
+    N, V = passes[0][0].shape
+    ops.logprob_entropy(passes[0][0][:chunk], passes[0][1][:chunk])
+    evs = kernel_events(2 * (N // chunk))
+    torch.cuda.synchronize()
+    i = 0
+    for x, t in passes:
+        for s0 in range(0, N, chunk):
+            ops.time_next_launch(*evs[i])
+            ops.logprob_entropy(x[s0:s0 + chunk], t[s0:s0 + chunk])
+            i += 1
+    torch.cuda.synchronize()
+    us = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    avg = sum(us) / len(us)
+    nbytes = W.logprob_algorithmic_bytes(chunk, V, 2)
+    del passes
+    return {
+        "shape": [N, V], "passes": 2, "chunk_rows": chunk, "chunks": len(us),
+        "kernel": LOGPROB_KERNEL, "avg_us_per_chunk": round(avg, 2),
+        "total_ms_both_passes": round(sum(us) / 1e3, 3),
+        "tokens_per_s": round(2 * N / (sum(us) * 1e-6), 1),
+        "algorithmic_bytes_per_chunk": nbytes,
+        "gbs": round(nbytes / (avg * 1e-6) / 1e9, 1),
+        "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": profiled_traffic(LOGPROB_KERNEL + f" [{chunk}, {V}]"),
     }
 
 
@@ -493,14 +637,28 @@ def main() -> int:
     line["graspo_loss"] = time_graspo_loss(dev)
     line["decode_loop"] = time_decode_loop(dev)
     line["hidden_logprobs"] = time_hidden_logprobs(dev)
+    flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
+    roof_s["stream_floor_us"] = round(stream_floor_us(wl.logits, flush), 2)
     if not args.no_per_config:
-        flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
-        line["per_config"] = {
-            f"sampler_{name}": time_sampler_config(cfg, dev, 20, flush)
-            for cfg, name in ((1, "fp32_8x151936"), (2, "bf16_64x151936_top_p"),
-                              (3, "bf16_64x151936_masked"))
+        topp = "sampler_topp_kernel<bf16>"
+        pc = {
+            f"sampler_{name}": time_sampler_config(cfg, dev, 20, flush, kernel)
+            for cfg, name, kernel in ((1, "fp32_8x151936", "sampler_split_kernel<fp32>"),
+                                      (2, "bf16_64x151936_top_p", topp + " penalty"),
+                                      (3, "bf16_64x151936_masked", topp + " mask"))
         }
-        del flush
+        pc["sampler_bf16_256x248320_decode_top_p"] = time_sampler_config(
+            5, dev, 20, flush, topp, override={"temperature": 0.7, "top_p": 0.9, "top_k": 0},
+            drop=("history", "allow_mask"),
+            what="the decode loop's rows: the [256,248320] logits, T 0.7, top-p 0.9, "
+                 "no top-k, history or mask")
+        pc["sampler_bf16_256x248320_masked_history_top_p"] = time_sampler_config(
+            5, dev, 20, flush, topp + " mask penalty", override={"top_k": 0},
+            what="configuration 5's inputs with top-k off (mask, history, penalty, "
+                 "T 0.7, top-p 0.9)")
+        pc["logprob_bf16_32768x151936"] = time_logprob_config4(dev)
+        line["per_config"] = pc
+    del flush
     if not args.no_cpu_baseline:
         cw = W.sampler_workload(5, device="cpu", rows=32)
         clx, clt = W.logprob_workload(5, device="cpu", rows=64)

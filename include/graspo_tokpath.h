@@ -348,14 +348,28 @@ int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
 
 /*
  * gtp_time_next_launch -- measurement hook, no counterpart in the reference:
- * the next gtp_sample_rows, gtp_logprob_entropy_rows or
- * gtp_logprob_backward_rows kernel launched from the calling thread records start_event when its dispatch begins and
+ * the next gtp_sample_rows, gtp_logprob_entropy_rows, gtp_logprob_backward_rows
+ * or gtp_stream_read_rows kernel launched from the calling thread records
+ * start_event when its dispatch begins and
  * stop_event when it ends (hipExtLaunchKernelGGL), so the two HIP events
  * bracket the kernel alone, without the idle time of event packets recorded
  * around it.  Both are hipEvent_t created by the caller (with timing).  The
  * hook is per thread and used once; the benchmark is its caller.
  */
 int gtp_time_next_launch(void* start_event, void* stop_event);
+
+/*
+ * gtp_stream_read_rows -- measurement helper, no counterpart in the
+ * reference: reads `rows` rows of `row_bytes` bytes (row_stride_bytes
+ * apart, all multiples of 16 from a 16-byte aligned `data`) once, with the
+ * samplers' access pattern (one 1024-thread workgroup per row, 16-byte
+ * non-temporal loads), and computes nothing else: the streaming floor the
+ * sampler kernels are measured against.  `out` ([rows] uint32) is written
+ * only for a row whose XOR of words equals 0x9E3779B9.  Goes through the
+ * gtp_time_next_launch hook.
+ */
+int gtp_stream_read_rows(const void* data, int64_t rows, int64_t row_bytes,
+                         int64_t row_stride_bytes, uint32_t* out, void* stream);
 
 /* Library version string, e.g. "graspo_tokpath 0.1 gfx950". */
 const char* gtp_version(void);
