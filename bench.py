@@ -159,15 +159,17 @@ def cpu_baseline(wl_cpu, lx_cpu, lt_cpu, min_seconds: float = 10.0):
 
 
 def profiled_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` as measured by rocprofv3 FETCH_SIZE
-    and WRITE_SIZE counters (scaled by the copy-kernel calibration), read from
-    the committed profile summary's ``traffic_bytes <kernel> <bytes>`` lines.
-    None when no such line exists."""
+    """HBM bytes per launch of ``kernel`` (a name, optionally with its
+    workload shape) as measured by rocprofv3 FETCH_SIZE and WRITE_SIZE
+    counters (scaled by the copy-kernel calibration), read from the committed
+    profile summary's ``traffic_bytes <key> <bytes>`` lines, whose key is the
+    name with spaces removed.  None when no such line exists."""
+    key = kernel.replace(" ", "")
     try:
         with open(TRAFFIC_FILE) as f:
             for ln in f:
                 parts = ln.strip().strip("`").split()
-                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == key:
                     return int(parts[2])
     except OSError:
         pass
