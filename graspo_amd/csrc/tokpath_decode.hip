@@ -77,6 +77,7 @@ extern "C" int gtp_decode_update_rows(int64_t* ids, const int32_t* status, int64
                                       int32_t* flags, void* stream) {
   if (B < 0 || col < 0 || !flags || (B > 0 && (!ids || !finished))) return GTP_ERR_INVALID_ARGUMENT;
   if ((seq && seq_stride <= col) || (attn && attn_stride <= col)) return GTP_ERR_INVALID_ARGUMENT;
+  if (B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(decode_update_kernel, dim3(1), dim3(kDuBlock), 0, s, ids, status, B,
                      eos_token_id, pad_token_id, finished, seq, seq_stride, attn, attn_stride, col,

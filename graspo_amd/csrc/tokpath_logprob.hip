@@ -421,6 +421,7 @@ extern "C" int gtp_lse_partial_rows(const void* logits, int dtype, int64_t N, in
 extern "C" int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_logprob,
                                      float* out_entropy, void* stream) {
   if (N < 0 || (N > 0 && !state)) return GTP_ERR_INVALID_ARGUMENT;
+  if (N > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   if (N == 0) return GTP_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)((N + 255) / 256);

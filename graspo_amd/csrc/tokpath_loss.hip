@@ -146,8 +146,8 @@ extern "C" int gtp_graspo_loss_backward(const float* logp, const float* old_logp
                                         float* grad_logp, void* stream) {
   if (B <= 0 || T <= 0 || !logp || !old_logp || !adv || !inv_denom || !grad_loss || !grad_logp)
     return GTP_ERR_INVALID_ARGUMENT;
+  if (T > (int64_t)0x7FFFFFFF * kLsBlock / B) return GTP_ERR_UNSUPPORTED;  // grid <= 2^31 - 1
   const int64_t n = B * T;
-  if ((n + kLsBlock - 1) / kLsBlock > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(graspo_loss_backward_kernel, dim3((unsigned)((n + kLsBlock - 1) / kLsBlock)),
                      dim3(kLsBlock), 0, s, logp, old_logp, adv, MaskIn{mask, mask_u8 ? 1 : 0},

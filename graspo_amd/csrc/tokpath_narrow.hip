@@ -54,6 +54,7 @@ using namespace gtp;
 extern "C" int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
                                      uint32_t* inexact, void* stream) {
   if (n < 0 || !inexact || (n > 0 && (!src || !dst))) return GTP_ERR_INVALID_ARGUMENT;
+  if (n > ((int64_t)1 << 56)) return GTP_ERR_UNSUPPORTED;  // beyond any address space
   if (n == 0) return GTP_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15u) == 0 &&

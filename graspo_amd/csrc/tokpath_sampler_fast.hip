@@ -1389,7 +1389,7 @@ using namespace gtp;
 
 extern "C" size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                              const gtp_sampler_params* params) {
-  if (!params || B <= 0 || V <= 0) return 0;
+  if (!params || B <= 0 || V <= 0 || V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, true);
   return pl.fast ? pl.ws_bytes : topp_workspace_bytes(dtype, B, V, params);
 }
@@ -1503,12 +1503,13 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
     return GTP_ERR_INVALID_ARGUMENT;
   if (B > 0 && (!logits || !out_ids)) return GTP_ERR_INVALID_ARGUMENT;
   if (!(params->repetition_penalty > 0.0f)) return GTP_ERR_INVALID_ARGUMENT;
+  // bounded before any size arithmetic below
+  if (V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   if (allow_mask && mask_stride < (V + 31) / 32) return GTP_ERR_INVALID_ARGUMENT;
   if (hist_len < 0) return GTP_ERR_INVALID_ARGUMENT;
   if (history && hist_len > 0 && hist_stride < hist_len) return GTP_ERR_INVALID_ARGUMENT;
   const bool greedy = !(params->temperature > 0.0f);
-  if (!greedy && !uniforms) return GTP_ERR_INVALID_ARGUMENT;
-  if (V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
+  if (!greedy && B > 0 && !uniforms) return GTP_ERR_INVALID_ARGUMENT;
   if (B == 0) return GTP_OK;
   SamplerArgs a;
   a.logits = logits;
@@ -1536,8 +1537,9 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 
   const int es = elem_size(dtype);
+  // the stride's byte count modulo 16, in unsigned arithmetic (any stride >= V is legal)
   const bool aligned = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 &&
-                       ((row_stride * es) & 15) == 0;
+                       (((uint64_t)row_stride * (uint64_t)es) & 15u) == 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, aligned);
   if (!pl.fast) {
     const size_t tw = topp_workspace_bytes(dtype, B, V, params);

@@ -197,15 +197,17 @@ int gtp_oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
                            float* out_sampled_logprob, int32_t* out_kept,
                            float* out_thresh_value, int32_t* out_thresh_id,
                            int32_t* out_status) {
-  if (!logits || !params || !out_ids || B < 0 || V <= 0 || row_stride < V)
+  if (!params || B < 0 || V <= 0 || row_stride < V || (B > 0 && (!logits || !out_ids)))
     return GTP_ERR_INVALID_ARGUMENT;
   if (dtype != GTP_DTYPE_F32 && dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F16)
     return GTP_ERR_INVALID_ARGUMENT;
   if (!(params->repetition_penalty > 0.0f)) return GTP_ERR_INVALID_ARGUMENT;
+  if (V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   if (allow_mask && mask_stride < (V + 31) / 32) return GTP_ERR_INVALID_ARGUMENT;
+  if (hist_len < 0) return GTP_ERR_INVALID_ARGUMENT;
   if (history && hist_len > 0 && hist_stride < hist_len) return GTP_ERR_INVALID_ARGUMENT;
   const int greedy = !(params->temperature > 0.0f);
-  if (!greedy && !uniforms) return GTP_ERR_INVALID_ARGUMENT;
+  if (!greedy && B > 0 && !uniforms) return GTP_ERR_INVALID_ARGUMENT;
   const float Tc = params->temperature > 1e-6f ? params->temperature : 1e-6f;
   const float rho = params->repetition_penalty;
   const int use_pen = history && hist_len > 0 && rho != 1.0f;
@@ -397,8 +399,11 @@ int gtp_oracle_logprob_entropy_rows(const void* logits, int dtype, int64_t N,
                                     const void* targets, int targets_int64,
                                     float* out_logprob, float* out_entropy,
                                     int32_t* out_status) {
-  if (!logits || !targets || !out_logprob || N < 0 || V <= 0 || row_stride < V)
+  if (N < 0 || V <= 0 || row_stride < V || (N > 0 && (!logits || !targets || !out_logprob)))
     return GTP_ERR_INVALID_ARGUMENT;
+  if (dtype != GTP_DTYPE_F32 && dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F16)
+    return GTP_ERR_INVALID_ARGUMENT;
+  if (N > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
   for (int64_t r = 0; r < N; ++r) {
     const int64_t base = r * row_stride;
     double M = -INFINITY;
