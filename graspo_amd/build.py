@@ -25,7 +25,7 @@ EXT_NAME = "_graspo_tokpath_ops"
 
 HIP_SOURCES = ["tokpath_logprob.hip", "tokpath_sampler.hip", "tokpath_sampler_fast.hip",
                "tokpath_loss.hip", "tokpath_decode.hip",
-               "tokpath_narrow.hip"]
+               "tokpath_narrow.hip", "tokpath_lmhead.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

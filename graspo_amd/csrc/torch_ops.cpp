@@ -1,7 +1,8 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
-// lse_finalize, decode_update, to_bf16_exact, logprob_backward_split, time_next_launch}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lse_finalize, decode_update, to_bf16_exact, logprob_backward_split, time_next_launch,
+// lm_head_logprob}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -432,6 +433,40 @@ void time_next_launch(int64_t start_event, int64_t stop_event) {
            "gtp_time_next_launch");
 }
 
+// logprob / entropy / lse of h W^T rows without the [N, V] logits: bf16
+// hidden [N, K] and weight [V, K] (rows contiguous, 16-byte aligned, K a
+// multiple of 128), targets int32/int64 [N].
+std::tuple<at::Tensor, at::Tensor, at::Tensor> lm_head_logprob(const at::Tensor& hidden,
+                                                               const at::Tensor& weight,
+                                                               const at::Tensor& targets,
+                                                               int64_t stream) {
+  for (const at::Tensor* t : {&hidden, &weight}) {
+    TORCH_CHECK(t->is_cuda(), "graspo_tokpath.lm_head_logprob: hidden / weight must be GPU tensors");
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16 && t->dim() == 2 && t->stride(1) == 1,
+                "graspo_tokpath.lm_head_logprob: hidden / weight must be bfloat16 2-D with "
+                "contiguous rows");
+  }
+  check_same_device(hidden, weight, "weight");
+  const int64_t N = hidden.size(0), K = hidden.size(1), V = weight.size(0);
+  TORCH_CHECK(weight.size(1) == K, "graspo_tokpath.lm_head_logprob: hidden is [N, ", K,
+              "] but weight is [V, ", weight.size(1), "]");
+  int t64 = 0;
+  const void* tp = targets_ptr(hidden, targets, N, &t64);
+  at::Tensor lp = at::empty({N}, hidden.options().dtype(at::kFloat));
+  at::Tensor H = at::empty({N}, lp.options());
+  at::Tensor lse = at::empty({N}, lp.options());
+  const size_t ws_bytes = gtp_lm_head_workspace_bytes(N, V);
+  at::Tensor ws = at::empty({(int64_t)ws_bytes}, hidden.options().dtype(at::kByte));
+  const int64_t ldh = N > 1 ? hidden.stride(0) : K, ldw = V > 1 ? weight.stride(0) : K;
+  const int rc = gtp_lm_head_logprob_rows(
+      reinterpret_cast<const uint16_t*>(hidden.data_ptr()), N, K, ldh,
+      reinterpret_cast<const uint16_t*>(weight.data_ptr()), V, ldw, tp, t64, lp.data_ptr<float>(),
+      H.data_ptr<float>(), lse.data_ptr<float>(), nullptr, ws.data_ptr(), ws_bytes,
+      reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_lm_head_logprob_rows");
+  return {lp, H, lse};
+}
+
 TORCH_LIBRARY(graspo_tokpath, m) {
   m.def(
       "sample(Tensor logits, float temperature, int top_k, float top_p, float repetition_penalty, "
@@ -469,4 +504,7 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "logprob_backward_split(Tensor logits, Tensor targets, Tensor grad_logprob, Tensor lse, "
       "int col_offset, int stream) -> (Tensor, Tensor)",
       &logprob_backward_split);
+  m.def("lm_head_logprob(Tensor hidden, Tensor weight, Tensor targets, int stream) -> "
+        "(Tensor, Tensor, Tensor)",
+        &lm_head_logprob);
 }

@@ -173,6 +173,28 @@ def lse_finalize(state: torch.Tensor):
     return ops.lse_finalize(state, _stream(state))
 
 
+def lm_head_supported(hidden: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether lm_head_logprob takes these bf16 operands: 2-D with contiguous,
+    16-byte aligned rows, K a multiple of 128 and row strides below 2^22."""
+    ok = (hidden.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and hidden.dim() == 2
+          and weight.dim() == 2 and hidden.size(1) == weight.size(1) and hidden.size(1) % 128 == 0
+          and hidden.size(1) > 0 and weight.size(0) > 0)
+    for t in (hidden, weight):
+        ok = ok and t.stride(1) == 1 and t.data_ptr() % 16 == 0
+        ok = ok and (t.size(0) <= 1 or (t.stride(0) % 8 == 0 and t.stride(0) < (1 << 22)))
+    return bool(ok)
+
+
+def lm_head_logprob(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor):
+    """(logprob, entropy, lse) [N] fp32 of the logits ``hidden @ weight.T``
+    without writing them: the bf16 GEMM on the matrix cores with the
+    log-sum-exp in its epilogue (bf16 ``hidden`` [N, K], ``weight`` [V, K],
+    ``lm_head_supported`` true)."""
+    ops = load()
+    targets = targets.reshape(-1).contiguous()
+    return ops.lm_head_logprob(hidden, weight, targets, _stream(hidden))
+
+
 def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torch.Tensor,
                   eos_token_id: int, pad_token_id: int, sequences: torch.Tensor | None,
                   attention_mask: torch.Tensor | None, col: int, flags: torch.Tensor) -> None:

@@ -222,6 +222,38 @@ int gtp_lse_finalize_rows(const float* state, int64_t N, float* out_logprob,
                           float* out_entropy, void* stream);
 
 /*
+ * gtp_lm_head_logprob_rows -- logprob, entropy and logsumexp of the logits
+ * x = h W^T per row without writing them: the bf16 lm_head GEMM runs on the
+ * matrix cores (fp32 accumulation) with the online log-sum-exp in its
+ * epilogue.
+ *
+ * Replaces _selected_token_log_probs_from_hidden
+ * src/graspo/backends/graspoflow/tensor_utils.py:167-186 (index_select of
+ * the target rows and their dot products, then F.linear + logsumexp +
+ * logaddexp per vocabulary chunk) for operands that are bf16 values.
+ *
+ *   hidden   [N, K] bf16, rows hidden_stride elements apart
+ *   weight   [V, K] bf16, rows weight_stride elements apart
+ *   targets  [N] int32 (targets_int64 == 0) or int64 token ids
+ *   out_logprob [N] = h_n . w_{t_n} - lse_n (the target logit is an fp32 dot
+ *            product of the exact bf16 products, as the reference's
+ *            selected_logits); out_entropy, out_lse [N] fp32 or NULL;
+ *            out_status [N] or NULL.  A target outside [0, V) gives NaN
+ *            logprob and GTP_ROW_BAD_TARGET.
+ *   workspace of at least gtp_lm_head_workspace_bytes(N, V) bytes (partial
+ *            states per vocabulary group; no contents carried between calls)
+ * Returns GTP_ERR_UNSUPPORTED unless K is a multiple of 128, both pointers
+ * are 16-byte aligned and both strides are multiples of 8 below 2^22.
+ */
+int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64_t K,
+                             int64_t hidden_stride, const uint16_t* weight, int64_t V,
+                             int64_t weight_stride, const void* targets, int targets_int64,
+                             float* out_logprob, float* out_entropy, float* out_lse,
+                             int32_t* out_status, void* workspace, size_t workspace_bytes,
+                             void* stream);
+size_t gtp_lm_head_workspace_bytes(int64_t N, int64_t V);
+
+/*
  * gtp_logprob_backward_rows -- gradient of log_softmax(x)[target] with respect
  * to the logits, scaled by the incoming gradient of each row:
  *   grad[i] = g * ([i == target - col_offset] - exp(x_i - lse))

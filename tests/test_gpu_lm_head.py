@@ -1,0 +1,109 @@
+"""GPU parity of the fused lm_head kernel (bf16 GEMM on the matrix cores
+with the log-sum-exp in its epilogue, gtp_lm_head_logprob_rows) against an
+fp64 evaluation of the reference's expression
+(_selected_token_log_probs_from_hidden, tensor_utils.py:167-186):
+logprob, entropy and logsumexp within 1e-4 absolute.
+
+Shapes cover vocabulary and token tails (V and N not multiples of the
+256 x 256 tile), a vocabulary smaller than one tile, one token, strided
+hidden rows, int32 and int64 targets, bad targets, large logits, and the
+full [8192, 4096] x [248320, 4096] case on sampled rows."""
+
+import pytest
+import torch
+
+from graspo_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def fp64_reference(h, w, t):
+    x = h.double() @ w.double().t()
+    lse = torch.logsumexp(x, dim=-1)
+    lp = x.gather(1, t.long().clamp(0, w.shape[0] - 1)[:, None])[:, 0] - lse
+    logp = x - lse[:, None]
+    ent = -(logp.exp() * logp).sum(-1)
+    return lp, ent, lse
+
+
+def _case(N, V, K, seed, scale=1.0, t64=False, hidden=None):
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    if hidden is None:
+        hidden = torch.randn(N, K, generator=g, device="cuda:0").to(torch.bfloat16)
+    w = (torch.randn(V, K, generator=g, device="cuda:0") * (scale / K ** 0.5)).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), generator=g, device="cuda:0",
+                      dtype=torch.int64 if t64 else torch.int32)
+    return hidden, w, t
+
+
+def _check(h, w, t, what):
+    print("lm_head:", what, tuple(h.shape), tuple(w.shape), flush=True)
+    assert ops.lm_head_supported(h, w)
+    lp, ent, lse = ops.lm_head_logprob(h, w, t)
+    torch.cuda.synchronize()
+    rlp, rent, rlse = fp64_reference(h, w, t)
+    for name, a, b in (("logprob", lp, rlp), ("entropy", ent, rent), ("lse", lse, rlse)):
+        err = (a.double() - b).abs().max().item()
+        assert err <= TOL, f"{what}: {name} differs by {err}"
+    return lp
+
+
+@pytest.mark.parametrize("N,V,K", [(300, 1037, 256), (1, 256, 128), (257, 300, 128),
+                                   (512, 100, 384), (1000, 40000, 1024), (256, 65536 + 255, 512)])
+def test_shapes_and_tails(N, V, K):
+    h, w, t = _case(N, V, K, seed=N + V + K)
+    _check(h, w, t, f"N {N} V {V} K {K}")
+
+
+def test_strided_hidden_and_int64_targets():
+    g = torch.Generator(device="cuda:0").manual_seed(3)
+    big = torch.randn(640, 1024 + 64, generator=g, device="cuda:0").to(torch.bfloat16)
+    h = big[:, 32:32 + 1024]  # rows 1088 elements apart, 64-byte offset
+    _, w, t = _case(640, 5000, 1024, seed=4, t64=True, hidden=h)
+    _check(h, w, t, "strided hidden, int64 targets")
+
+
+def test_large_logits():
+    """Logits of several hundred: the online max and the merge of partial
+    states across vocabulary groups must not overflow."""
+    h, w, t = _case(384, 20000, 512, seed=5, scale=60.0)
+    lp = _check(h, w, t, "large logits")
+    assert torch.isfinite(lp).all()
+
+
+def test_bad_targets_give_nan():
+    h, w, t = _case(64, 3000, 256, seed=6)
+    t[3] = -1
+    t[9] = 3000
+    lp, ent, lse = ops.lm_head_logprob(h, w, t)
+    torch.cuda.synchronize()
+    assert torch.isnan(lp[3]) and torch.isnan(lp[9])
+    assert torch.isfinite(lp[torch.arange(64, device=lp.device) % 3 == 1]).all()
+    assert torch.isfinite(ent).all() and torch.isfinite(lse).all()
+
+
+def test_full_size_sampled_rows():
+    """[8192, 4096] x [248320, 4096]: every row against the chunked
+    hipBLASLt + lse path within 1e-4, and 64 sampled rows against fp64."""
+    N, V, K = 8192, 248320, 4096
+    h, w, t = _case(N, V, K, seed=7, scale=4.0)
+    print("lm_head: full size", flush=True)
+    lp, ent, lse = ops.lm_head_logprob(h, w, t)
+    torch.cuda.synchronize()
+    rows = torch.randperm(N, generator=torch.Generator().manual_seed(8))[:64].to("cuda:0")
+    rlp, rent, rlse = fp64_reference(h[rows], w, t[rows])
+    for name, a, b in (("logprob", lp[rows], rlp), ("entropy", ent[rows], rent),
+                       ("lse", lse[rows], rlse)):
+        err = (a.double() - b).abs().max().item()
+        assert err <= TOL, f"full size: {name} differs by {err}"
+    # every row against the chunked path (fp32 logits from hipBLASLt, lse kernel)
+    state = ops.new_lse_state(N, h.device)
+    for c, start in enumerate(range(0, V, 32768)):
+        logits = torch.mm(h, w[start:start + 32768].t(), out_dtype=torch.float32)
+        ops.lse_partial(logits, t, start, state, accumulate=c > 0)
+        del logits
+    clp, cent = ops.lse_finalize(state)
+    assert (lp - clp).abs().max().item() <= 2 * TOL
+    assert (ent - cent).abs().max().item() <= 2 * TOL
