@@ -360,14 +360,15 @@ def time_graspo_loss(dev, B: int = 16, T: int = 2048, iters: int = 50):
 def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
     """The hidden-state logprob path at N tokens x H x V (tensor_utils.py:
     167-186 with the callers' fp32 copies of bf16 hidden states and lm_head,
-    qwen3/model.py:361-365): the drop-in (exact bf16 narrowing, bf16
-    matrix-core chunk GEMMs with fp32 logits, the lse kernel) against the
-    reference's expression in fp32 on the same device, plus the bf16 GEMM
-    alone over the same chunks (fp32 output), whose TFLOP/s are reported
-    against the 2.5 PFLOP/s dense bf16 peak."""
+    qwen3/model.py:361-365): the drop-in (exact bf16 narrowing, then the
+    fused bf16 GEMM + log-sum-exp kernel) against the reference's expression
+    in fp32 on the same device, the fused kernel's call on bf16 operands,
+    and hipBLASLt's bf16 GEMM alone over the reference's chunks (fp32
+    output); TFLOP/s are reported against the 2.5 PFLOP/s dense bf16 peak."""
     import torch
     import torch.nn.functional as F
 
+    from graspo_amd import ops
     from graspo_amd import tensor_utils as TU
 
     g = torch.Generator(device=dev).manual_seed(11)
@@ -393,6 +394,9 @@ def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
         for start in range(0, V, chunk):
             torch.mm(hb, wb[start:start + chunk].t(), out_dtype=torch.float32)
 
+    def fused():
+        return ops.lm_head_logprob(hb, wb, ids)
+
     def clock(fn, reps):
         fn()
         torch.cuda.synchronize()
@@ -406,6 +410,18 @@ def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
 
     ours_ms, lp = clock(dropin, 5)
     gemm_ms, _ = clock(gemm_only, 5)
+    fused_ms, _ = clock(fused, 5)
+    # the GEMM-with-lse kernel alone, HIP events from the dispatch itself
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    kern = []
+    for _ in range(5):
+        ops.time_next_launch(e0, e1)
+        fused()
+        torch.cuda.synchronize()
+        kern.append(e0.elapsed_time(e1))
+    kern_ms = sorted(kern)[len(kern) // 2]
     ref_ms, lp_ref = clock(reference, 2)
     # forward + backward (gradients of hidden and lm_head), as training uses it
     gout = torch.randn(N, device=dev, generator=g)
@@ -435,13 +451,19 @@ def time_hidden_logprobs(dev, N: int = 8192, H: int = 4096, V: int = 248320):
         "gemm_bf16_ms": round(gemm_ms, 3),
         "gemm_tflops": round(flops / (gemm_ms * 1e-3) / 1e12, 1),
         "gemm_frac_bf16_peak": round(flops / (gemm_ms * 1e-3) / 2.5e15, 4),
+        "fused_ms": round(fused_ms, 3), "fused_kernel_ms": round(kern_ms, 3),
+        "fused_tflops": round(flops / (fused_ms * 1e-3) / 1e12, 1),
+        "fused_frac_bf16_peak": round(flops / (fused_ms * 1e-3) / 2.5e15, 4),
         "dropin_tflops": round(flops / (ours_ms * 1e-3) / 1e12, 1),
         "max_abs_diff_vs_reference": round(float((lp - lp_ref).abs().max()), 7),
         "dropin_fwd_bwd_ms": round(ours_fb_ms, 3), "reference_fwd_bwd_ms": round(ref_fb_ms, 3),
         "max_abs_grad_diff_vs_reference": round(grad_diff, 9),
-        "what": "fp32 inputs holding bf16 values, as the callers pass them; HIP events, "
-                "5 (drop-in, GEMM) and 2 (reference) forward calls, 2 and 1 forward+backward "
-                "calls, each after one warm-up",
+        "what": "fp32 inputs holding bf16 values, as the callers pass them (the drop-in "
+                "narrows them, then runs the fused GEMM+lse kernel); fused = the kernel's "
+                "call on bf16 operands (GEMM+lse, target dots, merge), fused_kernel = the "
+                "GEMM+lse kernel alone; gemm_bf16 = hipBLASLt over the same chunks with fp32 "
+                "output; HIP events, 5 (drop-in, GEMM, fused) and 2 (reference) forward calls, "
+                "2 and 1 forward+backward calls, each after one warm-up",
     }
 
 

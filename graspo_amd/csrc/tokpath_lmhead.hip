@@ -13,11 +13,12 @@
 // Tile loop.  4 waves, 2 x 2 over the tile, each wave 128 x 128 (4 x 4 MFMA
 // blocks of 32 x 32, 256 fp32 accumulators per lane).  K advances 64 at a
 // time through two LDS stages of 32 KB per operand; the stage for step i+1
-// is loaded straight from global memory into LDS (global_load_lds_dwordx4,
-// no registers) while the matrix cores work on step i.  Each 128-byte LDS
-// row holds its eight 16-byte chunks XOR-swizzled by the row's low 3 bits,
-// so the MFMA operand reads (32 rows x one chunk per half-wave) hit 8
-// different chunk columns per 8 lanes.
+// is loaded straight from global memory into LDS (buffer_load_dwordx4 ...
+// lds, no registers) while the matrix cores work on step i.  Each 128-byte
+// LDS row holds its eight 16-byte chunks XOR-swizzled by bits 1-3 of the
+// row index: an MFMA operand read takes one chunk from each of 16
+// consecutive rows per 16 lanes, and (row & 1, chunk) then covers all 16
+// 16-byte bank groups of the 64 banks once.
 //
 // The GEMM computes logits transposed, vocabulary x tokens: lane l of a
 // 32 x 32 block holds token (l mod 32) and 16 vocabulary rows, so a token's
@@ -27,12 +28,15 @@
 // Order of work.  The workgroup for (vocabulary group g, token tile j) runs
 // kTilesPerGroup vocabulary tiles in a row (its K loop runs on across the
 // tile boundary), merging each tile into its running state, and writes one
-// partial state per (g, wave half, token).  Workgroup b runs on XCD b mod 8;
-// the 32 workgroups that share an XCD's L2 at a time take the same
-// vocabulary group and consecutive token tiles, so each weight tile is
-// fetched into that L2 once and read by all of them.  A merge kernel folds
-// the partials and the target logits (one fp32 dot product per token, the
-// reference's own selected_logits) into logprob, entropy and lse.
+// partial state per (g, wave half, token).  Workgroup b = g * n_tt + j runs
+// on XCD b mod 8, so with 32 token tiles the 32 workgroups that share an
+// XCD's L2 at a time cover 8 vocabulary groups x 4 token tiles: 12 operand
+// tiles per K step come into that L2 (the fewest for 32 workgroups; a whole
+// vocabulary group per XCD would bring in 33), and the window of 8 groups
+// is read from HBM once (the hidden states stay in the last-level cache).
+// A merge kernel folds the partials and the target logits (one fp32 dot
+// product per token, the reference's own selected_logits) into logprob,
+// entropy and lse.
 #include "tokpath_stream.h"
 
 namespace gtp {
@@ -45,7 +49,6 @@ constexpr int kThreads = 256;            // 4 waves
 constexpr int kChunks = kBK / 8;         // 16-byte chunks per tile row
 constexpr int kStage = kBV * kChunks;    // 16-byte chunks per operand stage (32 KB)
 constexpr int kTilesPerGroup = 4;        // vocabulary tiles per workgroup
-constexpr int kXcds = 8;
 constexpr int kMaxLd = (1 << 22) - 1;    // row strides (elements): 256 rows fit a buffer range
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer: 32-bit data format, no swizzle
 
@@ -57,43 +60,79 @@ struct Args {
   const uint16_t* w;  // [V, K] bf16, row stride ldw
   const uint16_t* h;  // [N, K] bf16, row stride ldh
   int64_t V, N, K, ldw, ldh;
-  int n_vt, n_tt, n_vg;  // vocabulary tiles, token tiles, vocabulary groups
-  float4* partial;       // [2 * n_vg][N]: (m, s, t, 0), t in base-2 units
+  int n_vfull, n_tt, n_vg;  // full vocabulary tiles, token tiles, groups of full tiles
+  float4* partial;          // [2 * n_vg + 2][N]: (m, s, t, 0), t in base-2 units
 };
 
 // s_waitcnt vmcnt(0), the other counters untouched
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Merge of two (m, s, t) states (t in base-2 units) without branches: a
+// side whose maximum is below the other's scales by 2^dl, dl clamped at
+// -256 so that an empty side (m = -inf, s = t = 0) adds exactly zero.  NaN
+// sums stay NaN.
+__device__ __forceinline__ Lse3 merge_states(Lse3 a, Lse3 b) {
+  const float m = fmaxf(a.m, b.m);
+  const float da = a.m == m ? 0.0f : fmaxf((a.m - m) * kLog2e, -256.0f);
+  const float db = b.m == m ? 0.0f : fmaxf((b.m - m) * kLog2e, -256.0f);
+  const float fa = __builtin_amdgcn_exp2f(da), fb = __builtin_amdgcn_exp2f(db);
+  return Lse3{m, a.s * fa + b.s * fb,
+              fa * __builtin_fmaf(da, a.s, a.t) + fb * __builtin_fmaf(db, b.s, b.t)};
+}
+
+// An accumulator read straight from its AGPR (keeps the compiler from
+// copying every accumulator to VGPRs at once before the epilogue).
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
 
 // Lane l's value of lane l ^ 32.
 __device__ __forceinline__ float swap_halves(float v) {
   return __int_as_float(__shfl_xor(__float_as_int(v), 32, kWave));
 }
 
+// kTail = false: the full vocabulary tiles, kTilesPerGroup per workgroup.
+// kTail = true: the last, partial tile (V mod 256 rows), one per token tile,
+// its rows past V masked in the epilogue; its partials follow the groups'.
+template <bool kTail>
 __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) uint4 sA0[kStage], sA1[kStage], sB0[kStage], sB1[kStage];
 
-  // ---- which tile group: XCD-major, token tiles fastest within an XCD
+  // ---- which tiles: token tiles fastest
   const int b = blockIdx.x;
-  const int xcd = b % kXcds, j = b / kXcds;
-  const int tt = j % a.n_tt;
-  const int vg = (j / a.n_tt) * kXcds + xcd;
-  if (vg >= a.n_vg) return;
-  const int vt0 = vg * kTilesPerGroup;
-  const int ntiles = min(kTilesPerGroup, a.n_vt - vt0);
+  int tt, vg, vt0, ntiles;
+  if constexpr (kTail) {
+    tt = b;
+    vg = a.n_vg;
+    vt0 = a.n_vfull;
+    ntiles = 1;
+  } else {
+    tt = b % a.n_tt;
+    vg = b / a.n_tt;
+    vt0 = vg * kTilesPerGroup;
+    ntiles = min(kTilesPerGroup, a.n_vfull - vt0);
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wv = wave >> 1, wt = wave & 1;  // the wave's vocabulary and token halves
 
-  // ---- load addressing: wave w's instruction q fills tile rows
-  // (8w + q) * 8 + lane / 8, chunk (lane & 7) ^ (row & 7) -- the row's low
-  // 3 bits are lane / 8 for every q.  Buffer resources cover exactly the
-  // tile's valid rows: a row past N or V reads as out of range (no access)
-  // and its stale LDS values only reach outputs that are masked or dropped.
+  // ---- load addressing: wave w's instruction q fills the 1 KB of LDS that
+  // holds tile rows (8w + q) * 8 + lane / 8, physical chunk lane & 7, so the
+  // lane fetches logical chunk (lane & 7) ^ ((row >> 1) & 7); with row =
+  // 8(8w + q) + lane / 8 that is (lane & 7) ^ ((4 (q & 1) + lane / 16) & 7).
+  // Buffer resources cover exactly the tile's valid rows: a row past N or V
+  // reads as out of range (no access) and its stale LDS values only reach
+  // outputs that are masked or dropped.
   const int lrow = (wave * 8) * 8 + (lane >> 3);
-  const int lchunk = (lane & 7) ^ ((lane >> 3) & 7);
-  const uint32_t voff_h = (uint32_t)((lrow * a.ldh + lchunk * 8) * 2);
-  const uint32_t voff_w = (uint32_t)((lrow * a.ldw + lchunk * 8) * 2);
+  const int lchunk0 = (lane & 7) ^ ((lane >> 4) & 7);        // even q
+  const int lchunk1 = (lane & 7) ^ ((4 + (lane >> 4)) & 7);  // odd q
+  const uint32_t voff_h0 = (uint32_t)((lrow * a.ldh + lchunk0 * 8) * 2);
+  const uint32_t voff_h1 = (uint32_t)((lrow * a.ldh + lchunk1 * 8) * 2);
+  const uint32_t voff_w0 = (uint32_t)((lrow * a.ldw + lchunk0 * 8) * 2);
+  const uint32_t voff_w1 = (uint32_t)((lrow * a.ldw + lchunk1 * 8) * 2);
   const int64_t t_rows = min((int64_t)kBT, a.N - (int64_t)tt * kBT);
   const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.h + (int64_t)tt * kBT * a.ldh), (short)0, (int)(t_rows * a.ldh * 2), kRsrcWord3);
@@ -109,20 +148,30 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   int load_tile = 0;  // tile of the next stage to load
   set_tile(vt0);
 
-  auto issue = [&](int it, uint4* sa, uint4* sb) {
+  // Loads of step `it` into the stage (sa, sb): 16 buffer loads per wave
+  // (8 weight, 8 hidden), issued one at a time between the MFMAs of the
+  // step before, so that the vector-memory queue never holds the wave back
+  // from the matrix cores.  prepare() sets the tile's resource and returns
+  // the byte offset of the step's K range.
+  auto prepare = [&](int it) {
     const int tile = it / kt;
     if (tile != load_tile) {
       load_tile = tile;
       set_tile(vt0 + tile);
     }
-    const int k0b = (it - tile * kt) * kBK * 2;
-    // the whole offset goes in the VGPR operand: the range check covers it
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(sa + (wave * 8 + q) * 64), 16,
-                                               voff_w + (uint32_t)(q * 8 * a.ldw * 2 + k0b), 0, 0, 0);
+    return (it - tile * kt) * kBK * 2;
+  };
+  // the whole offset goes in the VGPR operand: the range check covers it
+  auto issue_one = [&](int j, uint4* sa, uint4* sb, int k0b) {
+    const int q = j >> 1;
+    if (j & 1) {
+      const uint32_t vh = (q & 1) ? voff_h1 : voff_h0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void*)(sb + (wave * 8 + q) * 64), 16,
-                                               voff_h + (uint32_t)(q * 8 * a.ldh * 2 + k0b), 0, 0, 0);
+                                               vh + (uint32_t)(q * 8 * a.ldh * 2 + k0b), 0, 0, 0);
+    } else {
+      const uint32_t vw = (q & 1) ? voff_w1 : voff_w0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(sa + (wave * 8 + q) * 64), 16,
+                                               vw + (uint32_t)(q * 8 * a.ldw * 2 + k0b), 0, 0, 0);
     }
   };
 
@@ -141,84 +190,128 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     rt[y] = 0.0f;
   }
 
-  // operand reads: row = 32-row block base + (lane & 31), chunk 2kk + lane/32,
-  // swizzled by the row's low 3 bits (= lane & 7)
+  // operand reads: row = 32-row block base + (lane & 31), logical chunk
+  // 2kk + lane / 32 at physical chunk ^ ((row >> 1) & 7) = ^ ((lane >> 1) & 7)
   const int rd_row = lane & 31;
-  auto compute = [&](const uint4* sa, const uint4* sb) {
+  // The fragments of step kk + 1 are read while the MFMAs of step kk run
+  // (registers double-buffered), so only the first step of a stage waits
+  // for LDS latency.
+  auto read_frags = [&](const uint4* sa, const uint4* sb, int kk, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
+    const int ch = (2 * kk + (lane >> 5)) ^ ((lane >> 1) & 7);
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+      fa[x] = __builtin_bit_cast(bf16x8, sa[(wv * 128 + x * 32 + rd_row) * kChunks + ch]);
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+      fb[y] = __builtin_bit_cast(bf16x8, sb[(wt * 128 + y * 32 + rd_row) * kChunks + ch]);
+  };
+  // One stage of MFMAs from (sa, sb); when `load` is set, the 16 loads of the
+  // next step into (na, nb) go out one per 4 MFMAs.
+  auto compute = [&](const uint4* sa, const uint4* sb, uint4* na, uint4* nb, bool load, int k0b) {
+    bf16x8 fa[2][4], fb[2][4];
+    read_frags(sa, sb, 0, fa[0], fb[0]);
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int ch = (2 * kk + (lane >> 5)) ^ (lane & 7);
-      bf16x8 fa[4], fb[4];
+      const int c = kk & 1;
+      if (kk + 1 < kBK / 16) read_frags(sa, sb, kk + 1, fa[c ^ 1], fb[c ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int x = 0; x < 4; ++x)
-        fa[x] = __builtin_bit_cast(bf16x8, sa[(wv * 128 + x * 32 + rd_row) * kChunks + ch]);
-#pragma unroll
-      for (int y = 0; y < 4; ++y)
-        fb[y] = __builtin_bit_cast(bf16x8, sb[(wt * 128 + y * 32 + rd_row) * kChunks + ch]);
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
+      for (int x = 0; x < 4; ++x) {
 #pragma unroll
         for (int y = 0; y < 4; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][x], fb[c][y], acc[x][y], 0, 0, 0);
+        if (load) issue_one(kk * 4 + x, na, nb, k0b);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
 
   // fold the finished tile into the running state and clear the accumulators;
-  // rows past V (the last tile only) read as -inf, without a branch
+  // in the tail kernel rows past V read as -inf.  A lane folds its 64 values
+  // of a token one 16-value MFMA block at a time (online: a block with a new
+  // maximum rescales (s, t) by 2^dl), so only 16 accumulators are held in
+  // VGPRs at a time; then the two lane halves and the running state merge.
+  // The loop over the 4 token blocks is not unrolled (the unrolled form runs
+  // once per tile from a cold instruction cache): each trip folds block 0
+  // and rotates the blocks (and the running states) down by one, so after 4
+  // trips the accumulators are zero and the states are back in place.
   auto epilogue = [&](int tile) {
-    const int64_t vb = (int64_t)(vt0 + tile) * kBV + wv * 128 + 4 * (lane >> 5);
-    const int lim = (int)min((int64_t)128, max(a.V - vb, (int64_t)0));  // valid row offsets < lim
+    // the accumulators are read by inline asm, which the compiler's hazard
+    // checks do not see: 24 wait states after the last MFMA cover its
+    // result latency
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    int lim = 128;  // valid row offsets of this lane half are < lim
+    if constexpr (kTail) {
+      const int64_t vb = (int64_t)(vt0 + tile) * kBV + wv * 128 + 4 * (lane >> 5);
+      lim = (int)min((int64_t)128, max(a.V - vb, (int64_t)0));
+    }
+#pragma unroll 1
+    for (int r = 0; r < 4; ++r) {
+      float m = kNegInf, s = 0.0f, t = 0.0f;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      float xv[64];
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
+      for (int x = 0; x < 4; ++x) {
+        float v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int r = x * 32 + 8 * (i >> 2) + (i & 3);
-          xv[x * 16 + i] = r < lim ? acc[x][y][i] : kNegInf;
+          v[i] = acc_read(acc[x][0][i]);
+          if constexpr (kTail)
+            if (x * 32 + 8 * (i >> 2) + (i & 3) >= lim) v[i] = kNegInf;
         }
-      float m = kNegInf;
+        float cm = v[0];
 #pragma unroll
-      for (int e = 0; e < 64; e += 2) m = max3raw(m, xv[e], xv[e + 1]);
-      m = fmaxf(m, swap_halves(m));
-      // a wave whose rows are all past V folds nothing (m stays -inf)
-      const float mb = m == kNegInf ? 0.0f : m * kLog2e;
-      float s = 0.0f, t = 0.0f;
+        for (int i = 1; i < 16; i += 2) cm = max3raw(cm, v[i], i + 1 < 16 ? v[i + 1] : v[i]);
+        const float mn = fmaxf(m, cm);
+        // rescale the running sums to the new maximum (2^-256 flushes an
+        // empty start to zero without an inf * 0)
+        const float dl = m == mn ? 0.0f : fmaxf((m - mn) * kLog2e, -256.0f);
+        const float f = __builtin_amdgcn_exp2f(dl);
+        t = f * __builtin_fmaf(dl, s, t);
+        s *= f;
+        m = mn;
+        const float mb = m == kNegInf ? 0.0f : m * kLog2e;
 #pragma unroll
-      for (int e = 0; e < 64; ++e) {
-        const float d = __builtin_fmaf(xv[e], kLog2e, -mb);
-        const float p = __builtin_amdgcn_exp2f(d);
-        s += p;
-        t = __builtin_fmaf(p, fmaxf(d, -256.0f), t);
+        for (int i = 0; i < 16; ++i) {
+          const float d = __builtin_fmaf(v[i], kLog2e, -mb);
+          const float p = __builtin_amdgcn_exp2f(d);
+          s += p;
+          t = __builtin_fmaf(p, fmaxf(d, -256.0f), t);
+        }
       }
-      s += swap_halves(s);
-      t += swap_halves(t);
-      const Lse3 mg = lse3_merge(Lse3{rm[y], rs[y], rt[y]}, Lse3{m, s, t});
-      rm[y] = mg.m;
-      rs[y] = mg.s;
-      rt[y] = mg.t;
+      Lse3 st = merge_states(Lse3{m, s, t}, Lse3{swap_halves(m), swap_halves(s), swap_halves(t)});
+      st = merge_states(Lse3{rm[0], rs[0], rt[0]}, st);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) acc[x][y] = f32x16{};
+      for (int y = 0; y < 3; ++y) {
+        rm[y] = rm[y + 1];
+        rs[y] = rs[y + 1];
+        rt[y] = rt[y + 1];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) acc[x][y] = acc[x][y + 1];
+      }
+      rm[3] = st.m;
+      rs[3] = st.s;
+      rt[3] = st.t;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) acc[x][3] = f32x16{};
     }
   };
 
   // ---- main loop: k steps in pairs so that each LDS stage is a fixed array;
-  // the last pair of a tile prefetches the next tile's first stage
-  issue(0, sA0, sB0);
+  // the last step of a tile prefetches the next tile's first step
+  {
+    const int k0b = prepare(0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) issue_one(j, sA0, sB0, k0b);
+  }
   for (int tile = 0; tile < ntiles; ++tile) {
     for (int k = 0; k < kt; k += 2) {
       const int it = tile * kt + k;
       wait_vm0();
       __syncthreads();
-      issue(it + 1, sA1, sB1);
-      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the stage's math
-      compute(sA0, sB0);
+      compute(sA0, sB0, sA1, sB1, true, prepare(it + 1));
       wait_vm0();
       __syncthreads();
-      if (it + 2 < total) issue(it + 2, sA0, sB0);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(sA1, sB1);
+      const bool more = it + 2 < total;
+      compute(sA1, sB1, sA0, sB0, more, more ? prepare(it + 2) : 0);
     }
     epilogue(tile);
   }
@@ -299,16 +392,18 @@ __global__ __launch_bounds__(256) void lm_head_merge_kernel(const float4* __rest
 }
 
 struct Plan {
-  int n_vt, n_tt, n_vg;
+  int n_vfull, n_tt, n_vg;
+  bool tail;
   size_t partial_bytes, xt_bytes;
 };
 
 inline Plan plan(int64_t N, int64_t V) {
   Plan p;
-  p.n_vt = (int)((V + kBV - 1) / kBV);
+  p.n_vfull = (int)(V / kBV);
+  p.tail = V % kBV != 0;
   p.n_tt = (int)((N + kBT - 1) / kBT);
-  p.n_vg = (p.n_vt + kTilesPerGroup - 1) / kTilesPerGroup;
-  p.partial_bytes = ((size_t)2 * p.n_vg * (size_t)N * sizeof(float4) + 255) / 256 * 256;
+  p.n_vg = (p.n_vfull + kTilesPerGroup - 1) / kTilesPerGroup;
+  p.partial_bytes = ((size_t)(2 * p.n_vg + 2) * (size_t)N * sizeof(float4) + 255) / 256 * 256;
   p.xt_bytes = ((size_t)N * sizeof(float) + 255) / 256 * 256;
   return p;
 }
@@ -351,19 +446,22 @@ extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64
   a.K = K;
   a.ldw = weight_stride;
   a.ldh = hidden_stride;
-  a.n_vt = p.n_vt;
+  a.n_vfull = p.n_vfull;
   a.n_tt = p.n_tt;
   a.n_vg = p.n_vg;
   a.partial = reinterpret_cast<float4*>(workspace);
   float* xt = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + p.partial_bytes);
-  const int64_t per_xcd = ((int64_t)p.n_vg + lmh::kXcds - 1) / lmh::kXcds;
-  const int64_t grid = per_xcd * lmh::kXcds * p.n_tt;
+  const int64_t grid = (int64_t)p.n_vg * p.n_tt;
   if (grid > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
-  launch_timed(lmh::lm_head_lse_kernel, dim3((unsigned)grid), dim3(lmh::kThreads), s, a);
+  if (grid > 0) launch_timed(lmh::lm_head_lse_kernel<false>, dim3((unsigned)grid), dim3(lmh::kThreads), s, a);
+  if (p.tail)
+    hipLaunchKernelGGL(lmh::lm_head_lse_kernel<true>, dim3((unsigned)p.n_tt), dim3(lmh::kThreads), 0,
+                       s, a);
   hipLaunchKernelGGL(lmh::lm_head_target_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s,
                      weight, hidden, N, V, K, weight_stride, hidden_stride, targets, targets_int64,
                      xt);
   hipLaunchKernelGGL(lmh::lm_head_merge_kernel, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s,
-                     a.partial, 2 * p.n_vg, N, xt, out_logprob, out_entropy, out_lse, out_status);
+                     a.partial, 2 * p.n_vg + (p.tail ? 2 : 0), N, xt, out_logprob, out_entropy,
+                     out_lse, out_status);
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }

@@ -135,10 +135,12 @@ def _chunk_logits(h2, weight, mc, start, chunk):
 
 
 class _SelectedLogProbsFromHidden(torch.autograd.Function):
-    """log_softmax(h W^T)[target] without materialising [N, V] logits:
-    vocabulary chunks of the GEMM (bf16 matrix cores with fp32 output when
-    the operands are bf16 values) are folded into a running (m, s) state by
-    the lse kernel; the backward recomputes each chunk's softmax."""
+    """log_softmax(h W^T)[target] without materialising [N, V] logits.  When
+    the operands are bf16 values (K a multiple of 128) the forward is one
+    fused kernel: the bf16 GEMM on the matrix cores with the log-sum-exp in
+    its epilogue.  Otherwise vocabulary chunks of the GEMM are folded into a
+    running (m, s) state by the lse kernel.  The backward recomputes each
+    chunk's softmax."""
 
     @staticmethod
     def forward(ctx, hidden, weight, output_ids, chunk):
@@ -151,14 +153,19 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
             raise RuntimeError(
                 "_selected_token_log_probs_from_hidden: an output id is outside [0, vocab_size)")
         mc = _matrix_core_operands(h2, weight)
-        state = ops.new_lse_state(N, hidden.device)
-        # (running each chunk's lse on a second stream beside the next GEMM
-        # was slower: 21.4 against 16.5 ms at 8192 x 4096 x 248320)
-        for c, start in enumerate(range(0, V, chunk)):
-            logits = _chunk_logits(h2, weight, mc, start, chunk)
-            ops.lse_partial(logits, t, start, state, accumulate=c > 0)
-        lp, _ = ops.lse_finalize(state)
-        lse = state[:, 0] + torch.log(state[:, 1])
+        if N and mc is not None and ops.lm_head_supported(*mc):
+            # one kernel: the bf16 GEMM with the log-sum-exp in its epilogue,
+            # no [N, V] logits (the vocabulary chunking is the kernel's tiling)
+            lp, _, lse = ops.lm_head_logprob(mc[0], mc[1], t)
+        else:
+            state = ops.new_lse_state(N, hidden.device)
+            # (running each chunk's lse on a second stream beside the next
+            # GEMM was slower: 21.4 against 16.5 ms at 8192 x 4096 x 248320)
+            for c, start in enumerate(range(0, V, chunk)):
+                logits = _chunk_logits(h2, weight, mc, start, chunk)
+                ops.lse_partial(logits, t, start, state, accumulate=c > 0)
+            lp, _ = ops.lse_finalize(state)
+            lse = state[:, 0] + torch.log(state[:, 1])
         saved = (h2, weight, t, lse) + (mc if mc is not None else ())
         ctx.save_for_backward(*saved)
         ctx.has_mc = mc is not None
@@ -216,10 +223,13 @@ def _selected_token_log_probs_from_hidden(
     vocab_chunk_size: int = 32768,
 ) -> torch.Tensor:
     """logit[target] - logsumexp over the vocabulary, fp32 [*output_ids.shape]
-    (reference: tensor_utils.py:167-186).  The chunk loop keeps the
-    reference's ``vocab_chunk_size`` GEMMs -- on bf16 matrix cores with fp32
-    logits when the operands are bf16 values, as the reference's ``.float()``
-    copies are -- and the logsumexp / logaddexp fold is the lse kernel.
+    (reference: tensor_utils.py:167-186).  When the operands are bf16 values,
+    as the reference's ``.float()`` copies of bf16 tensors are, the forward
+    is one kernel: the bf16 GEMM on the matrix cores (fp32 accumulation) with
+    the logsumexp in its epilogue, and the target logit as an fp32 dot
+    product like the reference's ``selected_logits``.  Other operands keep
+    the reference's ``vocab_chunk_size`` GEMMs with the lse kernel as the
+    logsumexp / logaddexp fold.
     Differentiable in ``hidden_states`` and ``lm_head_weight``; on the bf16
     route the gradient GEMMs also run on matrix cores, with the fp32 softmax
     gradient split into two bf16 parts (hi + lo, within 2^-16 of it), so the

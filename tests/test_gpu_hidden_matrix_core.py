@@ -5,8 +5,9 @@ and flag exactly the inputs that are not bf16 values (nonzero lower bits,
 NaN payloads there included), for aligned, unaligned and ragged lengths.
 
 ``_selected_token_log_probs_from_hidden`` must take the bf16 route when its
-fp32 operands are bf16 values (as the reference's ``.float()`` copies are),
-stay in fp32 otherwise, and in every case agree with an fp64 evaluation of
+fp32 operands are bf16 values (as the reference's ``.float()`` copies are) --
+the fused GEMM + lse kernel when H is a multiple of 128, the chunked GEMMs
+otherwise -- stay in fp32 otherwise, and in every case agree with an fp64 evaluation of
 the reference expression (tensor_utils.py:167-186) within 1e-4 -- well inside
 the 1e-3 contract, since the bf16 x bf16 products are exact in fp32 and the
 logits are kept in fp32."""
@@ -79,6 +80,8 @@ def test_hidden_path_routes_and_accuracy(kind):
     h_in, w_in, ids_d = h_in.to(DEV), w_in.to(DEV), ids.to(DEV)
     mc = TU._matrix_core_operands(h_in.reshape(-1, H), w_in)
     assert (mc is not None) == (kind != "fp32_inexact")
+    # bf16 operands with H a multiple of 128 take the fused GEMM + lse kernel
+    assert (mc is not None and ops.lm_head_supported(*mc)) == (kind != "fp32_inexact")
     print("hidden route", kind, flush=True)
     out = TU._selected_token_log_probs_from_hidden(h_in, w_in, ids_d, vocab_chunk_size=4096)
     ref = _reference_fp64(h_in.cpu(), w_in.cpu(), ids)
