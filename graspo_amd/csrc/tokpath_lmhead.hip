@@ -48,7 +48,7 @@ constexpr int kBK = 64;                  // K per stage: 128 bytes of bf16 per r
 constexpr int kThreads = 256;            // 4 waves
 constexpr int kChunks = kBK / 8;         // 16-byte chunks per tile row
 constexpr int kStage = kBV * kChunks;    // 16-byte chunks per operand stage (32 KB)
-constexpr int kTilesPerGroup = 4;        // vocabulary tiles per workgroup
+constexpr int kTilesPerGroup = 2;        // vocabulary tiles per workgroup
 constexpr int kMaxLd = (1 << 22) - 1;    // row strides (elements): 256 rows fit a buffer range
 constexpr int kRsrcWord3 = 0x00020000;   // raw buffer: 32-bit data format, no swizzle
 
@@ -136,33 +136,22 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   const int64_t t_rows = min((int64_t)kBT, a.N - (int64_t)tt * kBT);
   const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.h + (int64_t)tt * kBT * a.ldh), (short)0, (int)(t_rows * a.ldh * 2), kRsrcWord3);
-  __amdgpu_buffer_rsrc_t rw;
-  auto set_tile = [&](int vt) {
-    const int64_t v_rows = min((int64_t)kBV, a.V - (int64_t)vt * kBV);
-    rw = __builtin_amdgcn_make_buffer_rsrc((void*)(a.w + (int64_t)vt * kBV * a.ldw), (short)0,
-                                           (int)(v_rows * a.ldw * 2), kRsrcWord3);
-  };
-
   const int kt = (int)(a.K / kBK);
   const int total = ntiles * kt;
-  int load_tile = 0;  // tile of the next stage to load
-  set_tile(vt0);
 
-  // Loads of step `it` into the stage (sa, sb): 16 buffer loads per wave
-  // (8 weight, 8 hidden), issued one at a time between the MFMAs of the
-  // step before, so that the vector-memory queue never holds the wave back
-  // from the matrix cores.  prepare() sets the tile's resource and returns
-  // the byte offset of the step's K range.
-  auto prepare = [&](int it) {
-    const int tile = it / kt;
-    if (tile != load_tile) {
-      load_tile = tile;
-      set_tile(vt0 + tile);
-    }
-    return (it - tile * kt) * kBK * 2;
+  // Loads of K step `it` (its weight tile's buffer resource and the byte
+  // offset of its K range): 16 buffer loads per wave, j even = weight rows,
+  // j odd = hidden rows, issued one per 2 MFMAs, so that the vector-memory
+  // queue never holds the wave back from the matrix cores.
+  auto w_rsrc = [&](int it) {
+    const int64_t vt = (int64_t)vt0 + it / kt;
+    const int64_t v_rows = min((int64_t)kBV, a.V - vt * kBV);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(a.w + vt * kBV * a.ldw), (short)0,
+                                             (int)(v_rows * a.ldw * 2), kRsrcWord3);
   };
+  auto k0b_of = [&](int it) { return (it % kt) * kBK * 2; };
   // the whole offset goes in the VGPR operand: the range check covers it
-  auto issue_one = [&](int j, uint4* sa, uint4* sb, int k0b) {
+  auto issue_one = [&](int j, __amdgpu_buffer_rsrc_t rw, int k0b, uint4* sa, uint4* sb) {
     const int q = j >> 1;
     if (j & 1) {
       const uint32_t vh = (q & 1) ? voff_h1 : voff_h0;
@@ -191,11 +180,10 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   }
 
   // operand reads: row = 32-row block base + (lane & 31), logical chunk
-  // 2kk + lane / 32 at physical chunk ^ ((row >> 1) & 7) = ^ ((lane >> 1) & 7)
+  // 2kk + lane / 32 at physical chunk ^ ((row >> 1) & 7) = ^ ((lane >> 1) & 7).
+  // The fragments of k16 step kk + 1 are read while the MFMAs of step kk run
+  // (registers double-buffered).
   const int rd_row = lane & 31;
-  // The fragments of step kk + 1 are read while the MFMAs of step kk run
-  // (registers double-buffered), so only the first step of a stage waits
-  // for LDS latency.
   auto read_frags = [&](const uint4* sa, const uint4* sb, int kk, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
     const int ch = (2 * kk + (lane >> 5)) ^ ((lane >> 1) & 7);
 #pragma unroll
@@ -205,25 +193,48 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     for (int y = 0; y < 4; ++y)
       fb[y] = __builtin_bit_cast(bf16x8, sb[(wt * 128 + y * 32 + rd_row) * kChunks + ch]);
   };
-  // One stage of MFMAs from (sa, sb); when `load` is set, the 16 loads of the
-  // next step into (na, nb) go out one per 4 MFMAs.
-  auto compute = [&](const uint4* sa, const uint4* sb, uint4* na, uint4* nb, bool load, int k0b) {
-    bf16x8 fa[2][4], fb[2][4];
-    read_frags(sa, sb, 0, fa[0], fb[0]);
+
+  // 16 MFMAs of one k16 step from fragment set c, with loads j0, j0 + 1, ...
+  // (weight resource rw, K offset k0b, into (la, lb)) after every second
+  // MFMA when `load` is set.
+  bf16x8 fa[2][4], fb[2][4];
+  auto mfma16 = [&](int c, bool load, int j0, __amdgpu_buffer_rsrc_t rw, int k0b, uint4* la,
+                    uint4* lb) {
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int c = kk & 1;
-      if (kk + 1 < kBK / 16) read_frags(sa, sb, kk + 1, fa[c ^ 1], fb[c ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int x = 0; x < 4; ++x) {
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][x], fb[c][y], acc[x][y], 0, 0, 0);
-        if (load) issue_one(kk * 4 + x, na, nb, k0b);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int y = 0; y < 4; ++y) {
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][x], fb[c][y], acc[x][y], 0, 0, 0);
+        if (load && (y & 1)) issue_one(j0 + x * 2 + (y >> 1), rw, k0b, la, lb);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  // K step `it` from LDS stage (cur_a, cur_b), whose first k16 fragments are
+  // already in set 0.  Step it + 1 lives in (nxt_a, nxt_b): its loads 0-7
+  // went out during the last k16 of step it - 1, its loads 8-15 go out
+  // during the first k16 here.  The barrier that publishes it sits before
+  // the last k16: every wave has read all of step it's fragments by then, so
+  // the loads 0-7 of step it + 2 into (cur_a, cur_b) go out during that last
+  // k16, while step it + 1's first fragments are read.
+  auto stage = [&](int it, uint4* cur_a, uint4* cur_b, uint4* nxt_a, uint4* nxt_b) {
+    const bool has1 = it + 1 < total, has2 = it + 2 < total;
+    const int i1 = has1 ? it + 1 : it, i2 = has2 ? it + 2 : it;
+    const __amdgpu_buffer_rsrc_t w1 = w_rsrc(i1), w2 = w_rsrc(i2);
+    read_frags(cur_a, cur_b, 1, fa[1], fb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16(0, has1, 8, w1, k0b_of(i1), nxt_a, nxt_b);
+    read_frags(cur_a, cur_b, 2, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16(1, false, 0, w1, 0, nxt_a, nxt_b);
+    read_frags(cur_a, cur_b, 3, fa[1], fb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16(0, false, 0, w1, 0, nxt_a, nxt_b);
+    wait_vm0();
+    __syncthreads();
+    if (has1) read_frags(nxt_a, nxt_b, 0, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16(1, has2, 0, w2, k0b_of(i2), cur_a, cur_b);
   };
 
   // fold the finished tile into the running state and clear the accumulators;
@@ -295,23 +306,24 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     }
   };
 
-  // ---- main loop: k steps in pairs so that each LDS stage is a fixed array;
-  // the last step of a tile prefetches the next tile's first step
+  // ---- main loop: K steps in pairs so that each LDS stage is a fixed array;
+  // the last steps of a tile load the next tile's first steps
   {
-    const int k0b = prepare(0);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) issue_one(j, sA0, sB0, k0b);
+    for (int j = 0; j < 16; ++j) issue_one(j, w_rsrc(0), k0b_of(0), sA0, sB0);
+    if (total > 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) issue_one(j, w_rsrc(1), k0b_of(1), sA1, sB1);
+    }
+    wait_vm0();
+    __syncthreads();
+    read_frags(sA0, sB0, 0, fa[0], fb[0]);
   }
   for (int tile = 0; tile < ntiles; ++tile) {
     for (int k = 0; k < kt; k += 2) {
       const int it = tile * kt + k;
-      wait_vm0();
-      __syncthreads();
-      compute(sA0, sB0, sA1, sB1, true, prepare(it + 1));
-      wait_vm0();
-      __syncthreads();
-      const bool more = it + 2 < total;
-      compute(sA1, sB1, sA0, sB0, more, more ? prepare(it + 2) : 0);
+      stage(it, sA0, sB0, sA1, sB1);
+      stage(it + 1, sA1, sB1, sA0, sB0);
     }
     epilogue(tile);
   }
