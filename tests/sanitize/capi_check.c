@@ -149,6 +149,41 @@ int main(void) {
   EXPECT_RC(w, gtp_stream_read_rows(A, INT64_MAX, 32, 32, out, NULL), X);
   EXPECT_RC(w, gtp_stream_read_rows(NULL, 0, 32, 32, NULL, NULL), OK);
 
+  const uint16_t* HB = PH(const uint16_t*);
+  const uint16_t* WB = (const uint16_t*)(uintptr_t)0x1000;
+  void* wsp = PH(void*);
+  const size_t wsz = gtp_lm_head_workspace_bytes(256, 1000);
+  EXPECT_RC(w, wsz > 0, 1);
+  EXPECT_RC(w, (int)gtp_lm_head_workspace_bytes(0, 1000), 0);
+  EXPECT_RC(w, (int)gtp_lm_head_workspace_bytes(256, 0), 0);
+  EXPECT_RC(w, (int)gtp_lm_head_workspace_bytes(INT64_MAX, 1000), 0);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, -1, 128, 128, WB, 1000, 128, T, 0, o, NULL, NULL, NULL,
+                                        wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 128, WB, 0, 128, T, 0, o, NULL, NULL, NULL,
+                                        wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 0, 128, WB, 1000, 128, T, 0, o, NULL, NULL, NULL,
+                                        wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 120, WB, 1000, 128, T, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(NULL, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 128, WB, 1000, 128, NULL, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL, NULL,
+                                        NULL, NULL, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz - 1, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 192, 192, WB, 1000, 192, T, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz, NULL), X);  /* K % 128 */
+  EXPECT_RC(w, gtp_lm_head_logprob_rows((const uint16_t*)(uintptr_t)0x18, 256, 128, 128, WB, 1000,
+                                        128, T, 0, o, NULL, NULL, NULL, wsp, wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, 256, 128, 1 << 22, WB, 1000, 128, T, 0, o, NULL, NULL,
+                                        NULL, wsp, wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(HB, INT64_MAX, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                        NULL, NULL, wsp, wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_rows(NULL, 0, 128, 128, NULL, 1000, 128, NULL, 0, NULL, NULL,
+                                        NULL, NULL, NULL, 0, NULL), OK);
+
   EXPECT_RC(w, strstr(gtp_version(), "gfx950") != NULL, 1);
 
   printf("C-ABI sanitizer checks: %d run, %d failed\n", g_checks, g_fails);
