@@ -103,6 +103,18 @@ __device__ __forceinline__ float block_max(SamplerSmem& sm, float v) {
   return r;
 }
 
+__device__ __forceinline__ unsigned long long block_max_u64(SamplerSmem& sm, unsigned long long v) {
+  v = wave_max_u64(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) sm.red_u[wid] = v;
+  __syncthreads();
+  unsigned long long r = sm.red_u[0];
+#pragma unroll
+  for (int w = 1; w < kSW; ++w) r = sm.red_u[w] > r ? sm.red_u[w] : r;
+  return r;
+}
+
 __device__ __forceinline__ uint32_t block_sum_u32(SamplerSmem& sm, uint32_t v) {
   v = wave_sum_u32(v);
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
@@ -652,10 +664,18 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
 
   // ================================================================ general
   __syncthreads();
-  // (A) exact max of the processed logits of valid tokens
+  // (A) exact max of the processed logits of valid tokens, and the row's
+  // last valid token in order (the lowest rank key): the last kept rank of
+  // a row with neither top-k nor top-p
   float ymax = kNegInf;
-  for_each_valid<T>(r, sm, [&](int32_t, float y, float) { ymax = fmaxf(ymax, y); });
+  unsigned long long nkey_last = 0ull;  // ~(lowest rank key)
+  for_each_valid<T>(r, sm, [&](int32_t id, float y, float) {
+    ymax = fmaxf(ymax, y);
+    const unsigned long long nk = ~rank_key(y, id);
+    nkey_last = nk > nkey_last ? nk : nkey_last;
+  });
   const float m = block_max(sm, ymax);
+  const unsigned long long key_last = ~block_max_u64(sm, nkey_last);
   if (m == kNegInf) {
     fail(GTP_ROW_EMPTY);
     return;
@@ -740,6 +760,10 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     Wk_hi = g.wcum[b_k];
   }
   int bp_lo = b_k, bp_hi = b_k;
+  // without top-k and top-p every valid token is kept: the last kept rank is
+  // key_last and the kept weight is W_all, so no bin needs collecting for
+  // the cut (the bottom bin can hold most of the row)
+  const bool keep_all = !r.greedy && !k_active && !p_active;
   if (p_active) {
     const int x1 = first_bin_w(floor_mul(a.P, Wk_lo));
     const int x2 = first_bin_w(floor_mul(a.P, Wk_hi));
@@ -748,9 +772,10 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   }
   int bu_lo = 0, bu_hi = bp_hi;
   if (!r.greedy) {
-    const unsigned long long Wp_lo = wex_bin(bp_lo);
+    unsigned long long Wp_lo = wex_bin(bp_lo);
     unsigned long long Wp_hi = g.wcum[bp_hi];
     if (Wp_hi > Wk_hi) Wp_hi = Wk_hi;
+    if (keep_all) Wp_lo = Wp_hi = W_all;
     const int y1 = first_bin_w(floor_mul(u, Wp_lo));
     const int y2 = first_bin_w(floor_mul(u, Wp_hi));
     bu_lo = y1 < bp_hi ? y1 : bp_hi;
@@ -759,8 +784,11 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     bu_lo = 0;
     bu_hi = 0;
   }
+  // the k cut's bin only matters with top-k (greedy: Keff = 1), the p cut's
+  // only when some rank can be cut
   auto in_need = [&](int bn) -> bool {
-    return bn == b_k || (bn >= bp_lo && bn <= bp_hi) || (bn >= bu_lo && bn <= bu_hi);
+    return (k_active && bn == b_k) || (!keep_all && bn >= bp_lo && bn <= bp_hi) ||
+           (bn >= bu_lo && bn <= bu_hi);
   };
   uint32_t need_local = 0;
   for (int bn = tid; bn < kNB; bn += kSB)
@@ -845,15 +873,19 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
       kept = 1;
       slp = 0.0;
     } else {
-      unsigned long long Wk = W_all;
+      unsigned long long Wk = W_all, Wp = W_all;
       if (k_active) Wk = g.cw[rank_lookup(nk - 1)];
-      int i_cut;
-      if (p_active) i_cut = first_above(floor_mul(a.P, Wk), nk);
-      else i_cut = rank_lookup(nk - 1);
-      const unsigned long long Wp = g.cw[i_cut];
-      kept = (int32_t)(g.crank[i_cut] + 1u);
-      id_thr = rank_key_id(g.ckey[i_cut]);
-      y_thr = rank_key_y(g.ckey[i_cut]);
+      if (keep_all) {
+        kept = (int32_t)n_valid;
+        id_thr = rank_key_id(key_last);
+        y_thr = rank_key_y(key_last);
+      } else {
+        const int i_cut = p_active ? first_above(floor_mul(a.P, Wk), nk) : rank_lookup(nk - 1);
+        Wp = g.cw[i_cut];
+        kept = (int32_t)(g.crank[i_cut] + 1u);
+        id_thr = rank_key_id(g.ckey[i_cut]);
+        y_thr = rank_key_y(g.ckey[i_cut]);
+      }
       const int i_u = first_above(floor_mul(u, Wp), (uint32_t)kept);
       id_draw = rank_key_id(g.ckey[i_u]);
       const unsigned long long w_u = detexp_fix(rank_key_y(g.ckey[i_u]) - m);

@@ -297,3 +297,25 @@ def test_greedy_non_finite_rows_under_mask_and_penalty(dtype):
         ref = oracle_sample(x, **kw)
         assert ref.ids[0] == 7 and ref.ids[2] == 77 and ref.ids[3] == 100 and ref.status[5] == 2
         assert_parity(got, ref, f"greedy masked V={V}")
+
+
+@pytest.mark.parametrize("kw", [dict(temperature=0.7, top_p=0.9), dict(temperature=0.7, top_p=1.0),
+                                dict(temperature=1.0, top_p=0.5, repetition_penalty=1.3),
+                                dict(temperature=0.7, top_k=300000, top_p=1.0)])
+def test_fp32_rows_that_are_not_bf16_values_full_vocab(kw):
+    """fp32 rows whose values are not bf16 values at V = 248320 (they take
+    the row-wise kernel's general path): N(0, 3) with spikes, T 0.7 spreads
+    the processed logits past the bins' 32-nat range, so the bottom bin
+    holds most of the row; with neither top-k nor top-p the last kept rank
+    is the row's last token, found without collecting that bin."""
+    B, V = 24, 248320
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(B, V, generator=g) * 3.0
+    x[:4, :3] += 12.0
+    assert bool((x.to(torch.bfloat16).float() != x).any())
+    u = torch.randint(0, 1 << 24, (B,), generator=g).float() * 2.0 ** -24
+    if "repetition_penalty" in kw:
+        kw = dict(kw, history=torch.randint(-1, V, (B, 1000), generator=g, dtype=torch.int32))
+    got = gpu_sample(x, uniforms=u, **kw)
+    ref = oracle_sample(x, uniforms=u, **kw)
+    assert_parity(got, ref, f"fp32 full vocab {kw.get('temperature')} {kw.get('top_p')}")
