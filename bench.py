@@ -237,16 +237,20 @@ def stream_floor_us(x, flush, iters: int = 10) -> float:
 
 
 def time_sampler_config(cfg: int, dev, iters: int, flush, kernel: str = SAMPLER_KERNEL,
-                        override: dict | None = None, drop: tuple = (), what: str | None = None):
+                        override: dict | None = None, drop: tuple = (), what: str | None = None,
+                        transform=None):
     """Average kernel time of one sampler launch on workload ``cfg`` (its
-    parameters changed by ``override``, inputs in ``drop`` removed) with the
-    MALL evicted before every launch."""
+    parameters changed by ``override``, inputs in ``drop`` removed, its
+    logits replaced by ``transform(logits)`` when given) with the MALL
+    evicted before every launch."""
     import torch
 
     from graspo_amd import ops
     from graspo_amd import workloads as W
 
     wl = W.sampler_workload(cfg, device=dev)
+    if transform is not None:
+        wl.logits = transform(wl.logits)
     kw = wl.kwargs()
     for k in drop:
         kw.pop(k, None)
@@ -680,6 +684,16 @@ def main() -> int:
             5, dev, 20, flush, topp + " mask penalty", override={"top_k": 0},
             what="configuration 5's inputs with top-k off (mask, history, penalty, "
                  "T 0.7, top-p 0.9)")
+        def fp32_inexact(x):
+            g = torch.Generator(device=x.device).manual_seed(5)
+            return x.float() + torch.rand(x.shape, generator=g, device=x.device) * 1e-3
+
+        pc["sampler_fp32_256x248320_decode_top_p"] = time_sampler_config(
+            5, dev, 5, flush, "sampler_rowwise_kernel<fp32>",
+            override={"temperature": 0.7, "top_p": 0.9, "top_k": 0},
+            drop=("history", "allow_mask"), transform=fp32_inexact,
+            what="fp32 rows that are not bf16 values (configuration 5's logits + U(0, 1e-3)), "
+                 "T 0.7, top-p 0.9: the row-wise kernel's general path")
         pc["logprob_bf16_32768x151936"] = time_logprob_config4(dev)
         line["per_config"] = pc
     del flush

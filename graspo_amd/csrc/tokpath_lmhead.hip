@@ -370,8 +370,10 @@ __global__ __launch_bounds__(256) void lm_head_target_kernel(const uint16_t* __r
   if (lane == 0) xt[n] = acc;
 }
 
-// Folds the 2 * n_vg partial states of each token: 64 tokens per workgroup,
-// 4 waves each merging a quarter of the partials, then one merge in LDS.
+// Folds the partial states of each token: 16 tokens per workgroup, 16
+// groups of threads each merging every 16th partial (a group reads 256
+// contiguous bytes per partial), then one merge in LDS.
+constexpr int kMergeTok = 16, kMergeGrp = 16;
 __global__ __launch_bounds__(256) void lm_head_merge_kernel(const float4* __restrict__ partial,
                                                             int nsub, int64_t N,
                                                             const float* __restrict__ xt,
@@ -379,22 +381,25 @@ __global__ __launch_bounds__(256) void lm_head_merge_kernel(const float4* __rest
                                                             float* __restrict__ out_H,
                                                             float* __restrict__ out_lse,
                                                             int32_t* __restrict__ out_status) {
-  __shared__ float red[4][64][3];
-  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  __shared__ float red[kMergeGrp][kMergeTok][3];
+  const int lt = threadIdx.x % kMergeTok, g = threadIdx.x / kMergeTok;
+  const int64_t n = (int64_t)blockIdx.x * kMergeTok + lt;
   Lse3 st{kNegInf, 0.0f, 0.0f};
-  if (n < N)
-    for (int p = g; p < nsub; p += 4) {
+  if (n < N) {
+#pragma unroll 4
+    for (int p = g; p < nsub; p += kMergeGrp) {
       const float4 v = partial[(int64_t)p * N + n];
-      st = lse3_merge(st, Lse3{v.x, v.y, v.z});
+      st = merge_states(st, Lse3{v.x, v.y, v.z});
     }
-  red[g][lane][0] = st.m;
-  red[g][lane][1] = st.s;
-  red[g][lane][2] = st.t;
+  }
+  red[g][lt][0] = st.m;
+  red[g][lt][1] = st.s;
+  red[g][lt][2] = st.t;
   __syncthreads();
   if (g != 0 || n >= N) return;
 #pragma unroll
-  for (int q = 1; q < 4; ++q) st = lse3_merge(st, Lse3{red[q][lane][0], red[q][lane][1], red[q][lane][2]});
+  for (int q = 1; q < kMergeGrp; ++q)
+    st = merge_states(st, Lse3{red[q][lt][0], red[q][lt][1], red[q][lt][2]});
   const float ln_s = __builtin_amdgcn_logf(st.s) * kLn2;
   const float x = xt[n];
   if (out_lp) out_lp[n] = raw_logprob(x, st.m, ln_s);
@@ -472,7 +477,8 @@ extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64
   hipLaunchKernelGGL(lmh::lm_head_target_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s,
                      weight, hidden, N, V, K, weight_stride, hidden_stride, targets, targets_int64,
                      xt);
-  hipLaunchKernelGGL(lmh::lm_head_merge_kernel, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s,
+  hipLaunchKernelGGL(lmh::lm_head_merge_kernel,
+                     dim3((unsigned)((N + lmh::kMergeTok - 1) / lmh::kMergeTok)), dim3(256), 0, s,
                      a.partial, 2 * p.n_vg + (p.tail ? 2 : 0), N, xt, out_logprob, out_entropy,
                      out_lse, out_status);
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
