@@ -291,6 +291,57 @@ __device__ __forceinline__ void for_each_valid(const Row<T>& r, const SamplerSme
   }
 }
 
+// Visit every group of 8 tokens that holds an allowed one: f(G, v[8], valid)
+// with, for kY, the processed logits y of all 8 (computed without a
+// per-element branch: a penalised and an unpenalised element differ in a
+// select) and `valid` the mask of the allowed tokens with y > -inf; without
+// kY, v holds the penalised logits x' before the temperature (no division)
+// and `valid` the allowed tokens with x' > -inf.  The loads run kAhead
+// groups ahead of their use (a pass over an fp32 batch re-reads it from
+// HBM: [256, 248320] fp32 outgrows the last-level cache).
+template <typename T, bool kY, typename F>
+__device__ __forceinline__ void for_each_group8(const Row<T>& r, const SamplerSmem& sm, F&& f) {
+  constexpr int kAhead = 3;
+  float xb[kAhead][8];
+  uint32_t mbb[kAhead];
+  auto fetch = [&](int64_t G, float (&x)[8], uint32_t& mb) {
+    mb = G < r.ngroups ? r.mask_byte(G) : 0u;
+    if (mb != 0u) load_group<T>(r.x, G, r.V, r.vec_ok, x);
+  };
+#pragma unroll
+  for (int q = 0; q < kAhead; ++q) fetch((int64_t)threadIdx.x + (int64_t)q * kSB, xb[q], mbb[q]);
+  for (int64_t G0 = threadIdx.x; G0 < r.ngroups; G0 += (int64_t)kAhead * kSB) {
+#pragma unroll
+    for (int q = 0; q < kAhead; ++q) {
+      const int64_t G = G0 + (int64_t)q * kSB;
+      const uint32_t mb = mbb[q];
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = xb[q][j];
+      fetch(G + (int64_t)kAhead * kSB, xb[q], mbb[q]);
+      if (mb == 0u) continue;
+      const uint32_t pb = r.pen_byte(sm, G);
+      if (pb != 0u) {  // (penalised tokens are rare: only their groups divide by rho)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float q2 = (x[j] < 0.0f) ? x[j] * r.rho : x[j] / r.rho;
+          x[j] = ((pb >> j) & 1u) ? q2 : x[j];
+        }
+      }
+      float v[8];
+      uint32_t valid = 0u;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float yy = kY ? (r.greedy ? x[j] : x[j] / r.Tc) + 0.0f : x[j];
+        v[j] = yy;
+        const bool ok = G * 8 + j < r.V && ((mb >> j) & 1u) && yy > kNegInf;
+        valid |= (ok ? 1u : 0u) << j;
+      }
+      f(G, v, valid);
+    }
+  }
+}
+
 // Write the outputs of a row.
 // (`fin`: the row's finished flag, read by the caller)
 __device__ __forceinline__ void write_row_f(const SamplerArgs& a, int64_t b, bool fin, int32_t status,
@@ -441,6 +492,7 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
   // ---- 1. stream pass
   LseState ls{kNegInf, 0.0f};
   float tl = kNegInf;
+  float xpmax = kNegInf;  // max of the allowed penalised logits x' (the general path's m)
   constexpr int64_t kStep = (int64_t)kSB * NG;
   for (int64_t base = 0; base < r.ngroups; base += kStep) {
     float x[NG][8];
@@ -477,7 +529,17 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
         cm = fmaxf(cm, ghi);
       }
       if (G < r.ngroups) sm.u.gkey[G] = (uint16_t)ord16(bf16_round_up(ghi));
-      if ((mb[k] & pb[k]) == 0u) tl = fmaxf(tl, ghi);
+      if ((mb[k] & pb[k]) == 0u) {
+        tl = fmaxf(tl, ghi);
+        xpmax = fmaxf(xpmax, ghi);
+      } else {  // (rare: a group with an allowed penalised token)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xj = x[k][j];
+          const float xp = ((pb[k] >> j) & 1u) ? ((xj < 0.0f) ? xj * r.rho : xj / r.rho) : xj;
+          if ((mb[k] >> j) & 1u) xpmax = fmaxf(xpmax, xp);
+        }
+      }
     }
     lse_fold<NG>(ls, x, cm);
   }
@@ -664,18 +726,14 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
 
   // ================================================================ general
   __syncthreads();
-  // (A) exact max of the processed logits of valid tokens, and the row's
-  // last valid token in order (the lowest rank key): the last kept rank of
-  // a row with neither top-k nor top-p
-  float ymax = kNegInf;
-  unsigned long long nkey_last = 0ull;  // ~(lowest rank key)
-  for_each_valid<T>(r, sm, [&](int32_t id, float y, float) {
-    ymax = fmaxf(ymax, y);
-    const unsigned long long nk = ~rank_key(y, id);
-    nkey_last = nk > nkey_last ? nk : nkey_last;
-  });
-  const float m = block_max(sm, ymax);
-  const unsigned long long key_last = ~block_max_u64(sm, nkey_last);
+  // (A) exact max of the processed logits of valid tokens.  Dividing by
+  // T > 0 with rounding to nearest is monotone, so the max of y = x' / T is
+  // the quotient of the max of x', taken in the stream pass: one division
+  // per row, no re-read.  (A token whose y alone overflows to -inf cannot
+  // hold the max unless every token does, and then the row is empty either
+  // way.)
+  const float xm = block_max(sm, xpmax);
+  const float m = (xm == kNegInf || r.greedy) ? xm : xm / r.Tc + 0.0f;
   if (m == kNegInf) {
     fail(GTP_ROW_EMPTY);
     return;
@@ -696,12 +754,29 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     const float d = (m - y) * kBinScale;
     return d < (float)(kNB - 1) ? (int)d : kNB - 1;
   };
-  for_each_valid<T>(r, sm, [&](int32_t, float y, float) {
-    const int bn = bin_of(y);
-    atomicAdd(&g.ccum[bn], 1u);
-    if (!r.greedy) atomicAdd(&g.wcum[bn], detexp_fix(y - m));
+  // (B), with the row's last valid token in order (the lowest rank key):
+  // the last kept rank of a row with neither top-k nor top-p (only looked
+  // for without top-p)
+  const bool want_last = !r.greedy && !p_active;
+  unsigned long long nkey_last = 0ull;  // ~(lowest rank key)
+  for_each_group8<T, true>(r, sm, [&](int64_t G, const float (&y)[8], uint32_t valid) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int bn = bin_of(y[j]);
+      // (a masked element's y may exceed m: its unused weight is taken at d <= 0)
+      const unsigned long long w = r.greedy ? 0ull : detexp_fix(fminf(y[j] - m, 0.0f));
+      const bool ok = (valid >> j) & 1u;
+      if (ok) {
+        atomicAdd(&g.ccum[bn], 1u);
+        if (!r.greedy) atomicAdd(&g.wcum[bn], w);
+      }
+      if (want_last) {
+        const unsigned long long nk = ok ? ~rank_key(y[j], (int32_t)(G * 8 + j)) : 0ull;
+        nkey_last = nk > nkey_last ? nk : nkey_last;
+      }
+    }
   });
-  __syncthreads();
+  const unsigned long long key_last = ~block_max_u64(sm, nkey_last);
   // inclusive prefix over bins: wave 0, 32 bins per lane
   if (tid < kWave) {
     constexpr int per = kNB / kWave;
@@ -802,14 +877,38 @@ __device__ __forceinline__ void rowwise_row(const SamplerArgs& a, int64_t b, Sam
     // (C) collect the needed bins and rank them exactly
     if (tid == 0) sm.ncand = 0;
     __syncthreads();
-    for_each_valid<T>(r, sm, [&](int32_t id, float y, float) {
-      const int bn = bin_of(y);
-      if (!in_need(bn)) return;
-      const int slot = atomicAdd(&sm.ncand, 1);
-      if (slot < kCollectCap) {
-        g.ckey[slot] = rank_key(y, id);
-        g.cw[slot] = r.greedy ? 0ull : detexp_fix(y - m);
-        g.cbin[slot] = (uint16_t)bn;
+    // the needed bins lie in [nb_lo, nb_hi]: y in (m - (nb_hi + 1) / 64,
+    // m - nb_lo / 64], widened by a bin and 2^-20 relative and mapped to x'
+    // (x' = y T up to rounding), so only tokens near those bins divide
+    int nb_lo = kNB, nb_hi = -1;
+    auto widen = [&](int lo, int hi) {
+      nb_lo = lo < nb_lo ? lo : nb_lo;
+      nb_hi = hi > nb_hi ? hi : nb_hi;
+    };
+    if (k_active) widen(b_k, b_k);
+    if (!keep_all) widen(bp_lo, bp_hi);
+    widen(bu_lo, bu_hi);
+    const float y_hi = m - (float)nb_lo / kBinScale + 1.0f / kBinScale;
+    const float y_lo = nb_hi >= kNB - 1 ? kNegInf : m - (float)(nb_hi + 2) / kBinScale;
+    auto pad = [](float v, float dir) { return v + dir * (fabsf(v) * 0x1p-20f + 0x1p-100f); };
+    const float sc = r.greedy ? 1.0f : r.Tc;
+    const float x_hi = pad(pad(y_hi, 1.0f) * sc, 1.0f);
+    const float x_lo = y_lo == kNegInf ? kNegInf : pad(pad(y_lo, -1.0f) * sc, -1.0f);
+    for_each_group8<T, false>(r, sm, [&](int64_t G, const float (&xp)[8], uint32_t valid) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (!((valid >> j) & 1u) || xp[j] < x_lo || xp[j] > x_hi) continue;
+        const float y = (r.greedy ? xp[j] : xp[j] / r.Tc) + 0.0f;
+        if (!(y > kNegInf)) continue;
+        const int bn = bin_of(y);
+        if (in_need(bn)) {
+          const int slot = atomicAdd(&sm.ncand, 1);
+          if (slot < kCollectCap) {
+            g.ckey[slot] = rank_key(y, (int32_t)(G * 8 + j));
+            g.cw[slot] = r.greedy ? 0ull : detexp_fix(y - m);
+            g.cbin[slot] = (uint16_t)bn;
+          }
+        }
       }
     });
     __syncthreads();
