@@ -45,7 +45,14 @@ namespace lmh {
 constexpr int kBV = 256;                 // vocabulary rows per tile
 constexpr int kBT = 256;                 // tokens per tile
 constexpr int kBK = 64;                  // K per stage: 128 bytes of bf16 per row
-constexpr int kThreads = 256;            // 4 waves
+// 2 x 2 waves of 128 x 128 (2 x 4 waves of 128 x 64, two per SIMD, measured
+// the same: 13.33 against 13.26 ms)
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kWTn = kWaves / 2;          // waves along the tokens (2 along the vocabulary)
+constexpr int kXB = 4;                    // 32-row vocabulary blocks per wave
+constexpr int kYB = 256 / 32 / kWTn;      // 32-token blocks per wave
+constexpr int kQ = 32 / kWaves;           // 1 KB loads per wave per operand and K step
 constexpr int kChunks = kBK / 8;         // 16-byte chunks per tile row
 constexpr int kStage = kBV * kChunks;    // 16-byte chunks per operand stage (32 KB)
 constexpr int kTilesPerGroup = 2;        // vocabulary tiles per workgroup
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wv = wave >> 1, wt = wave & 1;  // the wave's vocabulary and token halves
+  const int wv = wave / kWTn, wt = wave % kWTn;  // the wave's vocabulary half and token part
 
   // ---- load addressing: wave w's instruction q fills the 1 KB of LDS that
   // holds tile rows (8w + q) * 8 + lane / 8, physical chunk lane & 7, so the
@@ -126,7 +133,7 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   // Buffer resources cover exactly the tile's valid rows: a row past N or V
   // reads as out of range (no access) and its stale LDS values only reach
   // outputs that are masked or dropped.
-  const int lrow = (wave * 8) * 8 + (lane >> 3);
+  const int lrow = (wave * kQ) * 8 + (lane >> 3);
   const int lchunk0 = (lane & 7) ^ ((lane >> 4) & 7);        // even q
   const int lchunk1 = (lane & 7) ^ ((4 + (lane >> 4)) & 7);  // odd q
   const uint32_t voff_h0 = (uint32_t)((lrow * a.ldh + lchunk0 * 8) * 2);
@@ -155,25 +162,25 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     const int q = j >> 1;
     if (j & 1) {
       const uint32_t vh = (q & 1) ? voff_h1 : voff_h0;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void*)(sb + (wave * 8 + q) * 64), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void*)(sb + (wave * kQ + q) * 64), 16,
                                                vh + (uint32_t)(q * 8 * a.ldh * 2 + k0b), 0, 0, 0);
     } else {
       const uint32_t vw = (q & 1) ? voff_w1 : voff_w0;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(sa + (wave * 8 + q) * 64), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(sa + (wave * kQ + q) * 64), 16,
                                                vw + (uint32_t)(q * 8 * a.ldw * 2 + k0b), 0, 0, 0);
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[kXB][kYB];
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < kXB; ++x)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = f32x16{};
+    for (int y = 0; y < kYB; ++y) acc[x][y] = f32x16{};
 
   // running (m, s, t) of the wave's 4 tokens (t in base-2 units)
-  float rm[4], rs[4], rt[4];
+  float rm[kYB], rs[kYB], rt[kYB];
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
+  for (int y = 0; y < kYB; ++y) {
     rm[y] = kNegInf;
     rs[y] = 0.0f;
     rt[y] = 0.0f;
@@ -184,28 +191,28 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   // The fragments of k16 step kk + 1 are read while the MFMAs of step kk run
   // (registers double-buffered).
   const int rd_row = lane & 31;
-  auto read_frags = [&](const uint4* sa, const uint4* sb, int kk, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
+  auto read_frags = [&](const uint4* sa, const uint4* sb, int kk, bf16x8 (&fa)[kXB], bf16x8 (&fb)[kYB]) {
     const int ch = (2 * kk + (lane >> 5)) ^ ((lane >> 1) & 7);
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < kXB; ++x)
       fa[x] = __builtin_bit_cast(bf16x8, sa[(wv * 128 + x * 32 + rd_row) * kChunks + ch]);
 #pragma unroll
-    for (int y = 0; y < 4; ++y)
-      fb[y] = __builtin_bit_cast(bf16x8, sb[(wt * 128 + y * 32 + rd_row) * kChunks + ch]);
+    for (int y = 0; y < kYB; ++y)
+      fb[y] = __builtin_bit_cast(bf16x8, sb[(wt * kYB * 32 + y * 32 + rd_row) * kChunks + ch]);
   };
 
   // 16 MFMAs of one k16 step from fragment set c, with loads j0, j0 + 1, ...
   // (weight resource rw, K offset k0b, into (la, lb)) after every second
   // MFMA when `load` is set.
-  bf16x8 fa[2][4], fb[2][4];
+  bf16x8 fa[2][kXB], fb[2][kYB];
   auto mfma16 = [&](int c, bool load, int j0, __amdgpu_buffer_rsrc_t rw, int k0b, uint4* la,
                     uint4* lb) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < kXB; ++x) {
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
+      for (int y = 0; y < kYB; ++y) {
         acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[c][x], fb[c][y], acc[x][y], 0, 0, 0);
-        if (load && (y & 1)) issue_one(j0 + x * 2 + (y >> 1), rw, k0b, la, lb);
+        if (load && (y & 1)) issue_one(j0 + x * (kYB / 2) + (y >> 1), rw, k0b, la, lb);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     const __amdgpu_buffer_rsrc_t w1 = w_rsrc(i1), w2 = w_rsrc(i2);
     read_frags(cur_a, cur_b, 1, fa[1], fb[1]);
     __builtin_amdgcn_sched_barrier(0);
-    mfma16(0, has1, 8, w1, k0b_of(i1), nxt_a, nxt_b);
+    mfma16(0, has1, kQ, w1, k0b_of(i1), nxt_a, nxt_b);
     read_frags(cur_a, cur_b, 2, fa[0], fb[0]);
     __builtin_amdgcn_sched_barrier(0);
     mfma16(1, false, 0, w1, 0, nxt_a, nxt_b);
@@ -257,10 +264,10 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
       lim = (int)min((int64_t)128, max(a.V - vb, (int64_t)0));
     }
 #pragma unroll 1
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kYB; ++r) {
       float m = kNegInf, s = 0.0f, t = 0.0f;
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
+      for (int x = 0; x < kXB; ++x) {
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -291,18 +298,18 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
       Lse3 st = merge_states(Lse3{m, s, t}, Lse3{swap_halves(m), swap_halves(s), swap_halves(t)});
       st = merge_states(Lse3{rm[0], rs[0], rt[0]}, st);
 #pragma unroll
-      for (int y = 0; y < 3; ++y) {
+      for (int y = 0; y < kYB - 1; ++y) {
         rm[y] = rm[y + 1];
         rs[y] = rs[y + 1];
         rt[y] = rt[y + 1];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) acc[x][y] = acc[x][y + 1];
+        for (int x = 0; x < kXB; ++x) acc[x][y] = acc[x][y + 1];
       }
-      rm[3] = st.m;
-      rs[3] = st.s;
-      rt[3] = st.t;
+      rm[kYB - 1] = st.m;
+      rs[kYB - 1] = st.s;
+      rt[kYB - 1] = st.t;
 #pragma unroll
-      for (int x = 0; x < 4; ++x) acc[x][3] = f32x16{};
+      for (int x = 0; x < kXB; ++x) acc[x][kYB - 1] = f32x16{};
     }
   };
 
@@ -310,10 +317,10 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   // the last steps of a tile load the next tile's first steps
   {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) issue_one(j, w_rsrc(0), k0b_of(0), sA0, sB0);
+    for (int j = 0; j < 2 * kQ; ++j) issue_one(j, w_rsrc(0), k0b_of(0), sA0, sB0);
     if (total > 1) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) issue_one(j, w_rsrc(1), k0b_of(1), sA1, sB1);
+      for (int j = 0; j < kQ; ++j) issue_one(j, w_rsrc(1), k0b_of(1), sA1, sB1);
     }
     wait_vm0();
     __syncthreads();
@@ -331,8 +338,8 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   // ---- one partial state per (group, wave half, token), from lane half 0
   if (lane < 32) {
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      const int64_t n = (int64_t)tt * kBT + wt * 128 + y * 32 + lane;
+    for (int y = 0; y < kYB; ++y) {
+      const int64_t n = (int64_t)tt * kBT + wt * kYB * 32 + y * 32 + lane;
       if (n < a.N) a.partial[(int64_t)(vg * 2 + wv) * a.N + n] = float4{rm[y], rs[y], rt[y], 0.0f};
     }
   }
