@@ -255,8 +255,10 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   // trips the accumulators are zero and the states are back in place.
   auto epilogue = [&](int tile) {
     // the accumulators are read by inline asm, which the compiler's hazard
-    // checks do not see: 24 wait states after the last MFMA cover its
-    // result latency
+    // checks do not see: no MFMA may be scheduled past this point, and 24
+    // wait states after the last one cover its result latency (11 for an
+    // 8-pass MFMA)
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     int lim = 128;  // valid row offsets of this lane half are < lim
     if constexpr (kTail) {
