@@ -689,11 +689,11 @@ def main() -> int:
             return x.float() + torch.rand(x.shape, generator=g, device=x.device) * 1e-3
 
         pc["sampler_fp32_256x248320_decode_top_p"] = time_sampler_config(
-            5, dev, 5, flush, "sampler_rowwise_kernel<fp32>",
+            5, dev, 10, flush, "sampler_topp32_kernel<fp32>",
             override={"temperature": 0.7, "top_p": 0.9, "top_k": 0},
             drop=("history", "allow_mask"), transform=fp32_inexact,
             what="fp32 rows that are not bf16 values (configuration 5's logits + U(0, 1e-3)), "
-                 "T 0.7, top-p 0.9: the row-wise kernel's general path")
+                 "T 0.7, top-p 0.9: the fp32 top-p kernel (two reads of the rows)")
         pc["logprob_bf16_32768x151936"] = time_logprob_config4(dev)
         line["per_config"] = pc
     del flush

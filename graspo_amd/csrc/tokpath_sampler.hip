@@ -2062,34 +2062,46 @@ __global__ __launch_bounds__(kSB) void sampler_hist_kernel(SamplerArgs a) {
 }  // namespace gtp
 
 #include "tokpath_sampler_topp.h"
+#include "tokpath_sampler_topp32.h"
 
 using namespace gtp;
 
 namespace gtp {
 
-// The rows sampler_topp_kernel handed over (handover[0] of them, indices in
-// handover[1..]), on the row-wise path, one after another in one workgroup;
-// then the count and the list return to zero, so the workspace is all zero
-// again for the next call (the split kernel's arrival counters share it).
-// With no row handed over it reads one word and exits.
+// The rows a top-p kernel handed over (handover[0] of them, indices in
+// handover[2..]), on the row-wise path: workgroup i of a grid of B takes the
+// i-th listed row.  Every workgroup reads what it needs, then arrives at the
+// counter handover[1]; the last one returns the count, the counter and the
+// list to zero, so the workspace is all zero again for the next call (the
+// split kernel's arrival counters share its first 64 words, which every
+// kernel leaves zero).  With no row handed over each workgroup reads one word
+// and exits.
+template <typename T>
 __global__ __launch_bounds__(kSB) void sampler_handover_kernel(SamplerArgs a,
                                                                uint32_t* __restrict__ handover) {
   __shared__ SamplerSmem sm;
+  __shared__ uint32_t last;
   const uint32_t n = handover[0];
   if (n == 0u) return;
-  for (uint32_t i = 0; i < n; ++i) {
-    rowwise_row<uint16_t>(a, (int64_t)handover[1 + i], sm);
-    __syncthreads();
+  const uint32_t i = blockIdx.x;
+  if (i < n) rowwise_row<T>(a, (int64_t)handover[2 + i], sm);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    last = atomicAdd(&handover[1], 1u) == gridDim.x - 1u ? 1u : 0u;
   }
-  for (uint32_t i = threadIdx.x; i <= n; i += kSB) handover[i] = 0u;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (uint32_t j = threadIdx.x; j < n + 2u; j += kSB) handover[j] = 0u;
 }
 
 size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p) {
   const bool top_p = p->top_p > 0.0f && p->top_p < 1.0f && (p->top_k <= 0 || (int64_t)p->top_k >= V);
-  if (dtype != GTP_DTYPE_BF16 || !(p->temperature > 0.0f) || !(p->temperature <= 1024.0f) ||
-      !top_p || V < topp::kMinV || V > GTP_SAMPLER_MAX_V || B <= 0)
+  if ((dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F32) || !(p->temperature > 0.0f) ||
+      !(p->temperature <= 1024.0f) || !top_p || V < topp::kMinV || V > GTP_SAMPLER_MAX_V || B <= 0)
     return 0;
-  return ((size_t)(B + 1) * 4 + 255) / 256 * 256;
+  return ((size_t)(B + 2) * 4 + 255) / 256 * 256;  // count, arrival counter, list
 }
 
 // One workgroup of 1024 threads per row; handles every row layout, vocabulary
@@ -2100,15 +2112,30 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   // bf16 sampling rows on 16-byte aligned rows take the value-histogram
   // kernel (temperature bounded so that distinct bf16 values keep distinct,
   // normal y = x / T)
+  const int64_t es = dtype == GTP_DTYPE_F32 ? 4 : 2;
   const bool aligned = (reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0 &&
-                       ((a.row_stride * 2) & 15) == 0;
+                       ((a.row_stride * es) & 15) == 0;
   // (penalised counts are 16-bit: at most 65535 history entries)
   // top-p rows without top-k: the single-read top-p kernel, then the
   // row-wise path for any row it hands over (the hand-over list lives in the
   // workspace; without one, the value-histogram kernel below takes the call)
   gtp_sampler_params p{a.T, a.K, a.P, a.rho};
   const size_t tw = topp_workspace_bytes(dtype, B, a.V, &p);
-  if (tw > 0 && aligned && a.hist_len <= 65535 && workspace && workspace_bytes >= tw) {
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_F32 && workspace && workspace_bytes >= tw) {
+    // fp32 top-p rows: two reads, the candidates of the cut in LDS
+    uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
+    const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
+    switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
+      case 0: launch_timed(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
+      case 1: launch_timed(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
+      case 2: launch_timed(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
+      default: launch_timed(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
+    }
+    hipLaunchKernelGGL(sampler_handover_kernel<float>, grid, block, 0, s, a, handover);
+    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+  }
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
+      workspace_bytes >= tw) {
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
     const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
     switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
@@ -2117,7 +2144,7 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
       case 2: launch_timed(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
       default: launch_timed(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
     }
-    hipLaunchKernelGGL(sampler_handover_kernel, dim3(1), block, 0, s, a, handover);
+    hipLaunchKernelGGL(sampler_handover_kernel<uint16_t>, grid, block, 0, s, a, handover);
     return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
   }
   if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&

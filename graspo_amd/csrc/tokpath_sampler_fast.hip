@@ -1377,7 +1377,11 @@ FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p,
   pl.S = (int)S;
   pl.vps = vps;
   if (S > 1) {
-    pl.cnt_bytes = (((size_t)B * 4 + 255) / 256) * 256;
+    // the arrival counters of every split call on this device (S > 1 needs
+    // B < CUs) lie in one fixed region before the slots: calls whose B
+    // differs never find another call's slot data in their counters
+    const int64_t nc = B > cus ? B : cus;
+    pl.cnt_bytes = (((size_t)nc * 4 + 255) / 256) * 256;
     pl.ws_bytes = pl.cnt_bytes + (size_t)B * S * kSlotBytes;
   }
   return pl;
@@ -1545,7 +1549,7 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
     const size_t tw = topp_workspace_bytes(dtype, B, V, params);
     if (clear_counters && tw > 0 && workspace && workspace_bytes >= tw)
       hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, st,
-                         reinterpret_cast<uint32_t*>(workspace), (int64_t)1);
+                         reinterpret_cast<uint32_t*>(workspace), (int64_t)2);
     return launch_sampler_general(a, dtype, B, st, workspace, workspace_bytes);
   }
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes))

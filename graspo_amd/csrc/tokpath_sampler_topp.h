@@ -1272,7 +1272,7 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
 }  // namespace topp
 
 // One row per workgroup.  A row outside the top-p path's bounds is handed
-// over: its index goes to handover[1 + n] with n = handover[0]++, and
+// over: its index goes to handover[2 + n] with n = handover[0]++, and
 // sampler_handover_kernel, launched right after on the same stream, runs the
 // row-wise path for the listed rows and returns the list to zero.  The
 // row-wise path's registers thus never weigh on this kernel.
@@ -1283,7 +1283,7 @@ __global__ __launch_bounds__(topp::kB) void sampler_topp_kernel(SamplerArgs a,
   __shared__ topp::Smem sm;
   const int64_t b = blockIdx.x;
   if (!topp::topp_row<kMode>(a, b, sm) && threadIdx.x == 0)
-    handover[1 + atomicAdd(handover, 1u)] = (uint32_t)b;
+    handover[2 + atomicAdd(handover, 1u)] = (uint32_t)b;
 }
 
 }  // namespace gtp
