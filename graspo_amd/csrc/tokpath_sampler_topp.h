@@ -1045,9 +1045,13 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
         }
       }
     }
-    if (c) {  // (LDS atomics: the 16 lanes of one range meet at one address)
-      atomicAdd(&sm.x.own.w[v >> 4], wv);
-      atomicAdd(&sm.x.own.c[v >> 4], c);
+    // the 16 lanes of a row of the wave share one owner (v >> 4): their sums
+    // (DPP), then one LDS atomic per row instead of 16 on one address
+    const unsigned long long rw = row_scan_u64(wv);
+    const uint32_t rc = row_scan_u32(c);
+    if ((lane & 15) == 15 && rc) {
+      atomicAdd(&sm.x.own.w[v >> 4], rw);
+      atomicAdd(&sm.x.own.c[v >> 4], rc);
     }
   }
   if (kPen && unowned) atomicOr(&sm.flags, 1u);
