@@ -17,15 +17,29 @@ from torch.nn import functional as F  # noqa: N812
 from . import ops
 
 
-def _bf16_when_exact(logits: torch.Tensor, temperature: float, top_k: int) -> torch.Tensor:
+def _fp32_top_p_kernel_takes(logits: torch.Tensor, temperature: float, top_k: int,
+                             top_p: float) -> bool:
+    """Whether an fp32 call goes to the fp32 top-p kernel: top-p alone on
+    16-byte aligned rows of 65536 <= V <= 2^18, 0 < T <= 1024."""
+    B, V = logits.shape
+    return (0.0 < top_p < 1.0 and (top_k <= 0 or top_k >= V) and 65536 <= V <= (1 << 18)
+            and temperature <= 1024.0 and logits.data_ptr() % 16 == 0
+            and (logits.stride(0) * 4) % 16 == 0 and logits.stride(1) == 1)
+
+
+def _bf16_when_exact(logits: torch.Tensor, temperature: float, top_k: int,
+                     top_p: float = 1.0) -> torch.Tensor:
     """fp32 rows as their bf16 copy when every value is a bf16 value -- the
     reference's callers pass ``logits.float()`` of a bf16 model -- and the
     call would otherwise take the row-wise kernel (sampling without a top-k
-    of at most 128): the value-histogram kernel takes bf16 rows only, and the
-    samples are the same because the float inputs are.  Costs one pass over
-    the rows and one host synchronisation."""
+    of at most 128, other than the top-p rows the fp32 top-p kernel reads
+    directly, which is faster than the narrowing and its host
+    synchronisation): the value-histogram kernel takes bf16 rows only, and
+    the samples are the same because the float inputs are.  Costs one pass
+    over the rows and one host synchronisation."""
     if (logits.dtype != torch.float32 or logits.dim() != 2 or not logits.is_cuda
-            or not temperature > 0 or 1 <= top_k <= 128):
+            or not temperature > 0 or 1 <= top_k <= 128
+            or _fp32_top_p_kernel_takes(logits, temperature, top_k, top_p)):
         return logits
     bf, inexact = ops.to_bf16_exact(logits)
     return bf if int(inexact) == 0 else logits
@@ -53,7 +67,7 @@ def _next_token_from_logits(
     holding bf16 values take the bf16 kernels when the status is checked
     (that check synchronises anyway)."""
     if check_status:
-        logits = _bf16_when_exact(logits, float(temperature), int(top_k))
+        logits = _bf16_when_exact(logits, float(temperature), int(top_k), float(top_p))
     out = ops.sample(
         logits,
         temperature=float(temperature),
