@@ -72,7 +72,11 @@ template <typename T>
 constexpr int kNPof = Elem<T>::kDtype == GTP_DTYPE_F16 ? 3 : 4;
 constexpr int kSel = 2048;                  // re-read list entries per round
 constexpr int kPenWords = kSliceVecs * 8 / 32 + 2;
-constexpr int kMaxSlices = 64;
+// at most 8 slices per row: with few rows (B <= 16) one slice of a row
+// streams fast enough on its own and merging more lists costs more than the
+// slices save (fp32 [8, 151936], top-k 50: 25-27 us for 1 to 8 slices, 34 us
+// for 20)
+constexpr int kMaxSlices = 8;
 constexpr size_t kSlotBytes = 16 + (size_t)kFastK * 16;
 
 struct SliceHead {
