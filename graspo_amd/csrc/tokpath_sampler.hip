@@ -2063,6 +2063,7 @@ __global__ __launch_bounds__(kSB) void sampler_hist_kernel(SamplerArgs a) {
 
 #include "tokpath_sampler_topp.h"
 #include "tokpath_sampler_topp32.h"
+#include "tokpath_sampler_topps.h"
 
 using namespace gtp;
 
@@ -2096,12 +2097,42 @@ __global__ __launch_bounds__(kSB) void sampler_handover_kernel(SamplerArgs a,
   for (uint32_t j = threadIdx.x; j < n + 2u; j += kSB) handover[j] = 0u;
 }
 
-size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p) {
+// Top-p rows without top-k that the top-p kernels take (bf16 or fp32).
+bool topp_takes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p) {
   const bool top_p = p->top_p > 0.0f && p->top_p < 1.0f && (p->top_k <= 0 || (int64_t)p->top_k >= V);
-  if ((dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F32) || !(p->temperature > 0.0f) ||
-      !(p->temperature <= 1024.0f) || !top_p || V < topp::kMinV || V > GTP_SAMPLER_MAX_V || B <= 0)
-    return 0;
-  return ((size_t)(B + 2) * 4 + 255) / 256 * 256;  // count, arrival counter, list
+  return (dtype == GTP_DTYPE_BF16 || dtype == GTP_DTYPE_F32) && p->temperature > 0.0f &&
+         p->temperature <= 1024.0f && top_p && V >= topp::kMinV && V <= GTP_SAMPLER_MAX_V && B > 0;
+}
+
+// the hand-over count, arrival counter and list
+size_t topp_list_bytes(int64_t B) { return ((size_t)(B + 2) * 4 + 255) / 256 * 256; }
+
+ToppSplit plan_topp_split(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap) {
+  ToppSplit pl{0, 0, 0};
+  if (dtype != GTP_DTYPE_BF16 || !topp_takes(dtype, B, V, p) || B > kToppSplitMaxB) return pl;
+  const int64_t nvec = V / 8;
+  int64_t S = (device_cus() + B - 1) / B;
+  if (S > topps::kMaxS) S = topps::kMaxS;
+  for (; S >= 2; --S) {
+    // slices start on allow-mask word boundaries: vps a multiple of 8 vectors
+    const int64_t vps = ((nvec + S - 1) / S + 7) / 8 * 8;
+    const int64_t se = (nvec + vps - 1) / vps;
+    const size_t hb = ((size_t)B * se * topps::kHdrWords * 4 + 255) / 256 * 256;
+    const size_t bytes = kWsZeroBytes + hb + (size_t)B * se * topps::kSlotWords * 4;
+    if (se >= 2 && bytes <= cap) {
+      pl.S = (int)se;
+      pl.vps = vps;
+      pl.bytes = bytes;
+      break;
+    }
+  }
+  return pl;
+}
+
+size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap) {
+  if (!topp_takes(dtype, B, V, p)) return 0;
+  const ToppSplit sp = plan_topp_split(dtype, B, V, p, cap);
+  return sp.S ? sp.bytes : topp_list_bytes(B);
 }
 
 // One workgroup of 1024 threads per row; handles every row layout, vocabulary
@@ -2120,11 +2151,32 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   // row-wise path for any row it hands over (the hand-over list lives in the
   // workspace; without one, the value-histogram kernel below takes the call)
   gtp_sampler_params p{a.T, a.K, a.P, a.rho};
-  const size_t tw = topp_workspace_bytes(dtype, B, a.V, &p);
+  const size_t tw = topp_takes(dtype, B, a.V, &p) ? topp_list_bytes(B) : 0;
+  const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
+  // (rows with a mask and no penalty: the split kernel gains nothing from
+  // 32 rows on, [64, 151936] 43.4 against 42.1 us)
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
+      (pen || !a.mask || B <= 32)) {
+    // few bf16 rows: each row split over S workgroups (the workspace holds
+    // their counters, headers and slots)
+    const ToppSplit sp = plan_topp_split(dtype, B, a.V, &p, workspace_bytes);
+    if (sp.S >= 2) {
+      unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+      const dim3 sgrid((unsigned)sp.S, (unsigned)B);
+      switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
+        case 0: launch_timed(sampler_topps_kernel<0>, sgrid, block, s, a, ws, sp.vps); break;
+        case 1: launch_timed(sampler_topps_kernel<1>, sgrid, block, s, a, ws, sp.vps); break;
+        case 2: launch_timed(sampler_topps_kernel<2>, sgrid, block, s, a, ws, sp.vps); break;
+        default: launch_timed(sampler_topps_kernel<3>, sgrid, block, s, a, ws, sp.vps); break;
+      }
+      hipLaunchKernelGGL(sampler_handover_kernel<uint16_t>, grid, block, 0, s, a,
+                         reinterpret_cast<uint32_t*>(workspace));
+      return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+    }
+  }
   if (tw > 0 && aligned && dtype == GTP_DTYPE_F32 && workspace && workspace_bytes >= tw) {
     // fp32 top-p rows: two reads, the candidates of the cut in LDS
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
-    const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
     switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
       case 0: launch_timed(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
       case 1: launch_timed(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
@@ -2137,7 +2189,6 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
       workspace_bytes >= tw) {
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
-    const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
     switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
       case 0: launch_timed(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
       case 1: launch_timed(sampler_topp_kernel<1>, grid, block, s, a, handover); break;

@@ -1386,6 +1386,7 @@ FastPlan plan_fast(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p,
     // differs never find another call's slot data in their counters
     const int64_t nc = B > cus ? B : cus;
     pl.cnt_bytes = (((size_t)nc * 4 + 255) / 256) * 256;
+    if (pl.cnt_bytes < kWsZeroBytes) pl.cnt_bytes = kWsZeroBytes;
     pl.ws_bytes = pl.cnt_bytes + (size_t)B * S * kSlotBytes;
   }
   return pl;
@@ -1399,7 +1400,7 @@ extern "C" size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                              const gtp_sampler_params* params) {
   if (!params || B <= 0 || V <= 0 || V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, true);
-  return pl.fast ? pl.ws_bytes : topp_workspace_bytes(dtype, B, V, params);
+  return pl.fast ? pl.ws_bytes : topp_workspace_bytes(dtype, B, V, params, SIZE_MAX);
 }
 
 namespace gtp {
@@ -1478,7 +1479,9 @@ extern "C" int gtp_sample_rows_noalloc(const void* logits, int dtype, int64_t B,
                                        int32_t* out_status, void* stream) {
   if (!params || B < 0 || V <= 0) return GTP_ERR_INVALID_ARGUMENT;
   if (B == 0) return GTP_OK;
-  const size_t need = gtp_sample_workspace_bytes(dtype, B, V, params);
+  size_t need = gtp_sample_workspace_bytes(dtype, B, V, params);
+  if (need > GTP_NOALLOC_SCRATCH_BYTES && !plan_fast(dtype, B, V, params, true).fast)
+    need = topp_workspace_bytes(dtype, B, V, params, GTP_NOALLOC_SCRATCH_BYTES);  // fewer slices
   if (need > GTP_NOALLOC_SCRATCH_BYTES) return GTP_ERR_UNSUPPORTED;
   void* ws = nullptr;
   if (need > 0) {
@@ -1550,10 +1553,13 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
                        (((uint64_t)row_stride * (uint64_t)es) & 15u) == 0;
   const FastPlan pl = plan_fast(dtype, B, V, params, aligned);
   if (!pl.fast) {
-    const size_t tw = topp_workspace_bytes(dtype, B, V, params);
-    if (clear_counters && tw > 0 && workspace && workspace_bytes >= tw)
-      hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, st,
-                         reinterpret_cast<uint32_t*>(workspace), (int64_t)2);
+    const size_t tw = topp_workspace_bytes(dtype, B, V, params, workspace_bytes);
+    if (clear_counters && tw > 0 && workspace && workspace_bytes >= tw) {
+      // the hand-over count and counter; with a split, the whole zero region
+      const int64_t nw = tw >= kWsZeroBytes ? (int64_t)(kWsZeroBytes / 4) : 2;
+      hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st,
+                         reinterpret_cast<uint32_t*>(workspace), nw);
+    }
     return launch_sampler_general(a, dtype, B, st, workspace, workspace_bytes);
   }
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes))

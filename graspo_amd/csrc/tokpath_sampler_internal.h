@@ -38,9 +38,35 @@ struct SamplerArgs {
 int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
                            void* workspace, size_t workspace_bytes);
 
-// Workspace of the top-p path for these parameters (0 when another path
-// takes the call): the hand-over count and list of rows.
-size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p);
+// The first kWsZeroBytes of a sampler workspace are words that every call
+// leaves zero: the top-p kernels' hand-over count, arrival counter and list
+// (words 0, 1, 2..), the split kernel's per-row arrival counters (words
+// 0..B-1, B < CUs) and the split top-p kernel's (word kToppSplitCtrWord + b).
+// The kernels' slot data lies after it, so a call never finds another call's
+// slot data in its counters.
+constexpr size_t kWsZeroBytes = 16384;
+constexpr uint32_t kToppSplitCtrWord = 2048;
+// rows a split top-p call may have (at 128 rows of 248320 the one-workgroup
+// kernel is faster: 46 against 50 us)
+constexpr int64_t kToppSplitMaxB = 64;
+
+// Compute units of the current device (cached per device).
+int64_t device_cus();
+
+// The split top-p kernel's launch for these parameters: S slices of vps
+// vectors per row and the workspace it needs, at most `cap` bytes (fewer
+// slices when more would not fit); S = 0 when the call does not take it.
+struct ToppSplit {
+  int S;
+  int64_t vps;
+  size_t bytes;
+};
+ToppSplit plan_topp_split(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap);
+
+// Workspace of the top-p path for these parameters within `cap` bytes (0
+// when another path takes the call): the split kernel's counters, headers
+// and slots, or the hand-over count and list of rows.
+size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap);
 
 // Greedy decoding (T <= 0) is the reference's logits.argmax(dim=-1)
 // (src/graspo/backends/graspoflow/tensor_utils.py:658) over the allowed

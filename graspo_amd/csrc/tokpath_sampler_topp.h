@@ -397,21 +397,34 @@ __device__ __forceinline__ bool in_level(const Level& L, bool pn, uint32_t h) {
   return h == (pn ? L.hp : L.hu);
 }
 
-// Ids of the two levels' wanted tokens by one more read of the row: wave w
-// walks the contiguous range w of 16, counts each level's tokens with packed
-// 16-bit compares (bit 15 of a half is set where the half equals the level's
-// pattern), keeps up to kRescanBuf matching ids per level in id order; the
-// wave whose range holds a wanted token reads it from its buffer, or walks
-// its range again when the buffer overflowed.  Writes sm.id_out[0..1].
+// Ids of the two levels' wanted tokens (rank k0 of level 0, k1 of level 1,
+// in id order) by one more read of the vectors [lo_a, hi_a) (and the
+// vocabulary tail when `tail_a`) -- or, when `two`, of [lo_a, hi_a) for
+// level 0 by waves 0-7 and [lo_b, hi_b) (tail_b) for level 1 by waves 8-15.
+// Each wave walks a contiguous part of its range, counts its levels' tokens
+// with packed 16-bit compares (bit 15 of a half is set where the half equals
+// the level's pattern), keeps up to kRescanBuf matching ids per level in id
+// order; the wave whose part holds a wanted token reads it from its buffer,
+// or walks its part again when the buffer overflowed.  Writes
+// sm.id_out[0..1].
 template <int kMode>
-__device__ __forceinline__ void rescan_ids(Smem& sm, const Row& r) {
+__device__ __forceinline__ void rescan_ids(Smem& sm, const Row& r, int64_t lo_a, int64_t hi_a,
+                                           bool tail_a, int64_t lo_b, int64_t hi_b, bool tail_b,
+                                           uint32_t k0, uint32_t k1, bool two) {
   constexpr bool kPen = (kMode & 1) != 0, kMask = (kMode & 2) != 0;
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const int64_t nvec = r.nvec, V = r.V;
-  const int64_t span = (nvec + kW - 1) / kW;
-  const int64_t v0 = wid * span < nvec ? wid * span : nvec;
-  const int64_t v1 = v0 + span < nvec ? v0 + span : nvec;
-  const Level L0 = sm.lv[0], L1 = sm.lv[1];
+  const int grp = two && wid >= kW / 2 ? 1 : 0;  // (wave-uniform)
+  const int ng = two ? kW / 2 : kW, wl = two ? wid % (kW / 2) : wid;
+  const bool want0 = !two || grp == 0, want1 = !two || grp == 1;
+  const int64_t lo = grp ? lo_b : lo_a, hi = grp ? hi_b : hi_a;
+  const bool tail_here = grp ? tail_b : tail_a;
+  const int64_t span = (hi - lo + ng - 1) / ng;
+  const int64_t v0 = lo + wl * span < hi ? lo + wl * span : hi;
+  const int64_t v1 = v0 + span < hi ? v0 + span : hi;
+  Level L0 = sm.lv[0], L1 = sm.lv[1];
+  if (!want0) L0.hu = L0.hp = kNone;
+  if (!want1) L1.hu = L1.hp = kNone;
   uint32_t* buf0 = sm.hist + (0 * kW + wid) * kRescanBuf;
   uint32_t* buf1 = sm.hist + (1 * kW + wid) * kRescanBuf;
   // a level's value in both halves (0xFFFF, a NaN pattern, matches nothing
@@ -462,7 +475,7 @@ __device__ __forceinline__ void rescan_ids(Smem& sm, const Row& r) {
       t1 |= (on && in_level(L1, pn, h)) ? 1u << j : 0u;
     }
   };
-  const bool has_tail = wid == kW - 1 && nvec * 8 < V;
+  const bool has_tail = tail_here && wl == ng - 1 && nvec * 8 < V;
   constexpr int64_t kStep = (int64_t)kWave * kRescanG;
   // append the set bits of mm (ids base + bit) at position ex onwards
   auto keep = [&](uint32_t* buf, uint32_t mm, uint32_t ex, int64_t base) {
@@ -512,7 +525,8 @@ __device__ __forceinline__ void rescan_ids(Smem& sm, const Row& r) {
   }
   __syncthreads();
   for (int l = 0; l < 2; ++l) {
-    const uint32_t k = l ? L1.k : L0.k;
+    if (!(l ? want1 : want0)) continue;
+    const uint32_t k = l ? k1 : k0;
     uint32_t before = 0u;
     for (int w = 0; w < wid; ++w) before += sm.scan_n[w][l];
     const uint32_t mine = sm.scan_n[wid][l];
@@ -1256,7 +1270,7 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     __syncthreads();
     if (sm.bad) return false;
   } else {
-    rescan_ids<kMode>(sm, r);
+    rescan_ids<kMode>(sm, r, 0, nvec, true, 0, 0, false, L0.k, L1.k, false);
   }
 
   // ---- 9. outputs (both ids found, or the row goes to the row-wise path)

@@ -71,13 +71,33 @@ class SampleBuffers:
 
 
 def sample_args(logits: torch.Tensor, *, temperature, top_k=0, top_p=1.0,
-                repetition_penalty=1.0, history=None, allow_mask=None, uniforms=None):
+                repetition_penalty=1.0, history=None, allow_mask=None, uniforms=None,
+                finished=None, pad_token_id=0):
     """Leading arguments of gtp_sample_rows / _noalloc for [B, V] logits with
-    contiguous rows; returns (args, params, B)."""
+    unit-stride rows (history and mask contiguous, finished uint8 or bool);
+    returns (args, params, B)."""
     B, V = logits.shape
     p = SamplerParams(float(temperature), int(top_k), float(top_p), float(repetition_penalty))
     hist_len = 0 if history is None else history.shape[1]
     mask_stride = 0 if allow_mask is None else allow_mask.shape[1]
     args = [ptr(logits), DTYPE[logits.dtype], B, V, logits.stride(0), ptr(history), hist_len,
-            hist_len, ptr(allow_mask), mask_stride, ptr(uniforms), ctypes.byref(p), None, 0]
+            hist_len, ptr(allow_mask), mask_stride, ptr(uniforms), ctypes.byref(p),
+            ptr(finished), int(pad_token_id)]
     return args, p, B
+
+
+def sample_small_workspace(logits: torch.Tensor, **kw):
+    """gtp_sample_rows with a fresh zeroed workspace of only the top-p
+    hand-over list's bytes (B + 2 words): a top-p call then takes the
+    one-workgroup top-p kernel whatever B is.  Returns the outputs on the
+    CPU as a dict of the SampleOutput fields."""
+    L = lib()
+    dev = logits.device
+    args, p, B = sample_args(logits, **kw)
+    nbytes = ((B + 2) * 4 + 255) // 256 * 256
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    out = SampleBuffers(B, dev)
+    rc = L.gtp_sample_rows(*args, *out.out_args(), ws.data_ptr(), nbytes, stream_handle())
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return out.cpu()

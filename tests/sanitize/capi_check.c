@@ -51,8 +51,14 @@ int main(void) {
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 4, 0, &topp), 0);
   EXPECT_RC(w, (int)(gtp_sample_workspace_bytes(1, INT64_MAX, 151936, &topp) != 0), 0);
   EXPECT_RC(w, (int)(gtp_sample_workspace_bytes(1, 64, INT64_MAX, &topp) != 0), 0);
-  /* top-p bf16 rows: the hand-over count and list, rounded to 256 bytes */
-  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 64, 151936, &topp), 512);
+  /* top-p rows of a large batch (and fp32 rows): the hand-over count and
+     list, rounded to 256 bytes */
+  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 256, 151936, &topp), 1280);
+  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(0, 64, 151936, &topp), 512);
+  /* bf16 top-p rows of a small batch, split over S = 4 workgroups per row
+     (no device here: 256 CUs assumed): 16 KB of counters, 64 x 4 headers of
+     64 bytes, 64 x 4 slots of 64 KB */
+  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 64, 151936, &topp), 16384 + 16384 + 64 * 4 * 65536);
   /* the library's own workspace is bounded */
   EXPECT_RC(w, gtp_sample_rows_noalloc(L, 1, (int64_t)1 << 30, 151936, 151936, NULL, 0, 0, NULL,
                                        0, F, &topp, NULL, 0, PH(int64_t*), NULL, NULL, NULL, NULL,

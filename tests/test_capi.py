@@ -198,13 +198,16 @@ RAW_CASES = [
     ("rand", 3, 40000, torch.bfloat16, dict(temperature=0.0), 1),   # greedy
     ("workload", 5, 256, {}),                                       # the large batch, S = 1
     ("rand", 17, 151936, torch.bfloat16, dict(temperature=0.8, top_k=128), 2),
-    ("workload", 3, 64, {}),                                        # top-p only: no workspace
+    ("workload", 3, 64, {}),                                        # top-p, S = 4 per row
     ("rand", 64, 151936, torch.float32, dict(temperature=1.0, top_k=9, top_p=0.5), 3),
     # a split call with more rows than the earlier ones: its arrival counters
     # reach past where a 64-row call's slots would start
     ("rand", 100, 151936, torch.bfloat16, dict(temperature=0.9, top_k=20), 4),
     ("rand", 40, 151936, torch.float32, dict(temperature=0.7, top_p=0.9), 5),  # fp32 top-p
     ("rand", 100, 151936, torch.bfloat16, dict(temperature=0.9, top_k=20), 6),
+    ("rand", 100, 151936, torch.bfloat16, dict(temperature=0.8, top_p=0.9), 7),  # one workgroup
+    ("rand", 5, 248320, torch.bfloat16, dict(temperature=0.7, top_p=0.95), 8),   # top-p, S = 8
+    ("rand", 64, 151936, torch.bfloat16, dict(temperature=0.9, top_k=40), 9),
 ]
 
 

@@ -17,6 +17,7 @@ import torch
 
 from graspo_amd import ops
 from graspo_amd import workloads as W
+from tests import _capi
 from tests._util import oracle_sample
 from tests.test_gpu_sampler import assert_parity, gpu_sample
 
@@ -36,12 +37,31 @@ def _u(B, g):
     return torch.randint(0, 1 << 24, (B,), generator=g).float() * 2.0 ** -24
 
 
+def one_workgroup_sample(x, **kw):
+    """The call through the C ABI with a workspace that holds only the
+    hand-over list, so that rows of a small batch take the one-workgroup
+    kernel instead of the split one."""
+    dev = torch.device("cuda:0")
+    kw = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    if kw.get("finished") is not None:
+        kw["finished"] = kw["finished"].to(torch.uint8)
+    xd = x.to(dev)
+    if xd.stride(1) != 1 or xd.data_ptr() % 16 != 0:
+        xd = aligned_rows(x)
+    out = _capi.sample_small_workspace(xd, **kw)
+    return ops.SampleOutput(*[out[f] for f in ops.SampleOutput._fields])
+
+
 def _check(x, what, **kw):
+    """Both kernels against the oracle: the torch op (rows of batches up to
+    128 split over several workgroups) and the one-workgroup kernel."""
     print("topp:", what, tuple(x.shape), {k: v for k, v in kw.items()
                                           if not isinstance(v, torch.Tensor)}, flush=True)
     g = gpu_sample(x, **kw)
     ref = oracle_sample(x, **kw)
     assert_parity(g, ref, what)
+    if x.shape[0] <= 128 and not kw.get("top_k"):
+        assert_parity(one_workgroup_sample(x, **kw), ref, what + " (one workgroup)")
     return g, ref
 
 
