@@ -672,7 +672,7 @@ def main() -> int:
         pc = {
             f"sampler_{name}": time_sampler_config(cfg, dev, 20, flush, kernel)
             for cfg, name, kernel in ((1, "fp32_8x151936", "sampler_split_kernel<fp32>"),
-                                      (2, "bf16_64x151936_top_p", topp + " penalty"),
+                                      (2, "bf16_64x151936_top_p", "sampler_topps_kernel<bf16> penalty"),
                                       (3, "bf16_64x151936_masked", topp + " mask"))
         }
         pc["sampler_bf16_256x248320_decode_top_p"] = time_sampler_config(
