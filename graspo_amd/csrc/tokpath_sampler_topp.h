@@ -252,10 +252,25 @@ __device__ __forceinline__ int ceil_v(const Row& r, float y) {
 }
 
 // First value bin p in [0, kNV] with ypen(p) <= y (ypen falls as p grows),
-// by the 64 lanes of a wave: rounds of 64 probes narrow 16128 candidates
-// to one in three steps.  Wave-uniform result.
+// by the 64 lanes of a wave.  First one window of 64 bins around the raw
+// value whose penalised, scaled logit is y (x = y T rho for y >= 0, y T / rho
+// below): the predicate "p == kNV or ypen(p) <= y" is monotone, so when the
+// window's first bin fails it (or is bin 0) and a later one passes, the
+// first passing bin is the answer.  Otherwise rounds of 64 probes narrow
+// 16128 candidates to one in three steps.  Wave-uniform result.
 __device__ __forceinline__ int first_pen_le(const Row& r, float y) {
   const int lane = threadIdx.x & (kWave - 1);
+  {
+    const float xs = y * r.Tc;
+    const int ve = vb_of(bf16_round_up(xs >= 0.0f ? xs * r.rho : xs / r.rho));
+    if (ve >= 0) {
+      int w0 = ve - kWave / 2;
+      w0 = w0 < 0 ? 0 : (w0 > kNV - (kWave - 1) ? kNV - (kWave - 1) : w0);
+      const int p = w0 + lane;  // <= kNV
+      const unsigned long long pass = __ballot(p >= kNV || r.ypen(p) <= y);
+      if (pass && (w0 == 0 || !(pass & 1ull))) return w0 + __builtin_ctzll(pass);
+    }
+  }
   int lo = 0, hi = kNV;  // the answer lies in [lo, hi]
   while (hi > lo) {
     const int span = hi - lo;
