@@ -126,6 +126,10 @@ struct alignas(16) Smem {
   float u;            // the row's uniform and finished flag (read at the start)
   uint32_t fin;
   uint32_t flags;     // bit 0: hand over; bit 1: bad history id
+  // the weight scan's totals (weight, count, region-2 count, raw (m, s))
+  unsigned long long tot_w;
+  uint32_t tot_n, tot_n2;
+  float tot_m, tot_s;
   int32_t bad;
   __device__ __forceinline__ uint32_t* pen() { return reinterpret_cast<uint32_t*>(&qd[kPoolVPen]); }
   __device__ __forceinline__ const uint32_t* pen() const {
@@ -215,6 +219,65 @@ __device__ __forceinline__ void block_scan2(Smem& sm, unsigned long long w, uint
   tw = allw;
   tc = allc;
   tf = allf;
+}
+
+// The weight step's block scan: exclusive prefix in thread order of the
+// owners' (weight, count), the totals, the sum of n2 and the raw (m, s)
+// merge (online with a mask and no penalty).  Wave 0 combines the 16 waves'
+// partials in its lanes and hands the prefixes back through LDS, so no
+// thread loops over all waves (the tail runs at one CU's issue rate).
+template <int kMode>
+__device__ __forceinline__ void weight_scan(Smem& sm, unsigned long long Wt, uint32_t Nt, uint32_t n2,
+                                            float lm, float lsum, unsigned long long& ew, uint32_t& ec,
+                                            unsigned long long& W, uint32_t& N, uint32_t& N2, float& lse_m,
+                                            float& lse_s) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const unsigned long long iw = wave_scan_u64(Wt);
+  const uint32_t ic = wave_scan_u32(Nt);
+  const uint32_t s2 = wave_sum_u32(n2);
+  if (kMode == 2) wave_lse2(lm, lsum);
+  else if (kMode != 3) lsum = wave_sum_f(lsum);
+  __syncthreads();  // (own is read)
+  if (lane == kWave - 1) {
+    sm.red_w[wid] = iw;
+    sm.red_u[wid][0] = ic;
+    sm.red_u[wid][1] = s2;
+    sm.red_f[wid][0] = lm;
+    sm.red_f[wid][1] = lsum;
+  }
+  __syncthreads();
+  if (wid == 0) {
+    const bool in = lane < kW;
+    const unsigned long long vw = in ? sm.red_w[lane] : 0ull;
+    const uint32_t vc = in ? sm.red_u[lane][0] : 0u, v2 = in ? sm.red_u[lane][1] : 0u;
+    const float fm = in ? sm.red_f[lane][0] : kNegInf, fs = in ? sm.red_f[lane][1] : 0.0f;
+    const unsigned long long pw = wave_scan_u64(vw);
+    const uint32_t pc = wave_scan_u32(vc);
+    const uint32_t t2 = wave_sum_u32(v2);
+    const float mm = wave_max_f(fm);
+    float ss = 0.0f;
+    if (kMode == 2) ss = wave_sum_f(fs > 0.0f ? fs * __builtin_amdgcn_exp2f((fm - mm) * kLog2e) : 0.0f);
+    else if (kMode != 3) ss = wave_sum_f(fs);
+    if (in) {  // (this wave read its lanes' entries above)
+      sm.red_w[lane] = pw - vw;
+      sm.red_u[lane][2] = pc - vc;
+    }
+    if (lane == kWave - 1) {
+      sm.tot_w = pw;
+      sm.tot_n = pc;
+      sm.tot_n2 = t2;
+      sm.tot_m = mm;
+      sm.tot_s = ss;
+    }
+  }
+  __syncthreads();
+  ew = sm.red_w[wid] + iw - Wt;
+  ec = sm.red_u[wid][2] + ic - Nt;
+  W = sm.tot_w;
+  N = sm.tot_n;
+  N2 = sm.tot_n2;
+  lse_m = sm.tot_m;
+  lse_s = sm.tot_s;
 }
 
 struct Row {
@@ -1088,57 +1151,10 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
   if (kPen && (sm.flags & 1u)) return false;
   const unsigned long long Wt = sm.x.own.w[tid];
   const uint32_t Nt = sm.x.own.c[tid];
-  // block scan of (Wt, Nt) in thread order, with the sums of n2 and the
-  // (lm, lsum) merge
   unsigned long long ew, W;
   uint32_t ec, N, N2;
   float lse_m, lse_s;
-  {
-    const unsigned long long iw = wave_scan_u64(Wt);
-    const uint32_t ic = wave_scan_u32(Nt);
-    const uint32_t s2 = wave_sum_u32(n2);
-    if (kMode == 2) wave_lse2(lm, lsum);
-    else if (kMode != 3) lsum = wave_sum_f(lsum);
-    __syncthreads();  // (own is read)
-    if (lane == kWave - 1) {
-      sm.red_w[wid] = iw;
-      sm.red_u[wid][0] = ic;
-      sm.red_u[wid][1] = s2;
-      sm.red_f[wid][0] = lm;
-      sm.red_f[wid][1] = lsum;
-    }
-    __syncthreads();
-    unsigned long long bw = 0ull;
-    uint32_t bc = 0u;
-    W = 0ull;
-    N = N2 = 0u;
-    lse_m = kNegInf;
-#pragma unroll
-    for (int i = 0; i < kW; ++i) {
-      const unsigned long long vw = sm.red_w[i];
-      const uint32_t vc = sm.red_u[i][0];
-      if (i < wid) {
-        bw += vw;
-        bc += vc;
-      }
-      W += vw;
-      N += vc;
-      N2 += sm.red_u[i][1];
-      lse_m = sm.red_f[i][0] > lse_m ? sm.red_f[i][0] : lse_m;
-    }
-    lse_s = 0.0f;
-    if (kMode == 2) {
-#pragma unroll
-      for (int i = 0; i < kW; ++i)
-        if (sm.red_f[i][1] > 0.0f)
-          lse_s += sm.red_f[i][1] * __builtin_amdgcn_exp2f((sm.red_f[i][0] - lse_m) * kLog2e);
-    } else if (kMode != 3) {
-#pragma unroll
-      for (int i = 0; i < kW; ++i) lse_s += sm.red_f[i][1];
-    }
-    ew = bw + iw - Wt;
-    ec = bc + ic - Nt;
-  }
+  weight_scan<kMode>(sm, Wt, Nt, n2, lm, lsum, ew, ec, W, N, N2, lse_m, lse_s);
   // no penalty: every token is in a value bin (the counts add up)
   if (!kPen && N + N2 != (uint32_t)V) return false;
   sm.x.ex.w[tid] = ew;

@@ -55,6 +55,7 @@ struct Extra {
   uint32_t last;                  // this workgroup is the row's last to arrive
   int32_t sl[2];                  // slice of each wanted token
   uint32_t jl[2];                 // its rank among its value's tokens there
+  uint32_t pub[8];                // the slice's ranges, largest-value bins, tokens, escapes
 };
 
 // One workgroup's part of row b: slice s of S (vectors [s vps, (s+1) vps)).
@@ -150,8 +151,6 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
                   __attribute__((always_inline)) {
     constexpr bool partial = decltype(partial_c)::value;
     const uint32_t base = s0u + chunk * (uint32_t)kChunk;
-    float xf[kG][8];
-    float cm = kNegInf;
 #pragma unroll
     for (int k = 0; k < kG; ++k) {
       const uint32_t vi = base + (uint32_t)(k * kWave + lane);
@@ -179,16 +178,16 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
         lds_add(sm, a2 & 0xFFFFu, (neg & 0xFFFFu) + 1u);
         lds_add(sm, a2 >> 16, (neg >> 16) + 1u);
       }
-      if constexpr (kMode == 3) {
-        Vec<uint16_t>::cvt(buf[k], xf[k]);
+      if constexpr (kMode == 3) {  // (one vector at a time: 8 live floats, no spills)
+        float xk[1][8];
+        Vec<uint16_t>::cvt(buf[k], xk[0]);
         if (partial && !valid) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xf[k][j] = kNegInf;
+          for (int j = 0; j < 8; ++j) xk[0][j] = kNegInf;
         }
-        cm = max3raw(cm, vec_max<8>(xf[k]), kNegInf);
+        lse_fold_block_max<false, 1, 8>(st, xk, vec_max<8>(xk[0]));
       }
     }
-    if constexpr (kMode == 3) lse_fold_block_max<false, kG, 8>(st, xf, cm);
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
@@ -286,31 +285,47 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
       sm.red_u[wid][3] = (uint32_t)(pmax + 1) | ((uint32_t)nmin << 14) | (esc << 28);
     }
     __syncthreads();
-    // every thread: the two regions' ranges and summaries
-    uint32_t rg[2][2] = {{0xFFFFFFFFu, 0u}, {0xFFFFFFFFu, 0u}};
-    uint32_t top[2] = {(uint32_t)kNV, (uint32_t)kNV}, ntok = 0u, nesc = 0u;
+    // wave 0 combines the 16 waves' partials (lanes 0-7 region A, 8-15
+    // region 2) and hands the slice's summary to every thread
+    if (wid == 0) {
+      const bool in = lane < kW;
+      uint32_t rlo = in ? sm.red_u[lane][0] : 0xFFFFFFFFu, rhi = in ? sm.red_u[lane][1] : 0u;
+      uint32_t nt = in ? sm.red_u[lane][2] : 0u;
+      const uint32_t pk = in ? sm.red_u[lane][3] : (kNI << 14);
+      int pm = (int)(pk & 0x3FFFu) - 1, nm = (int)((pk >> 14) & 0x3FFFu);
+      uint32_t es = pk >> 28;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      int pm = -1, nm = (int)kNI;
-#pragma unroll
-      for (int i = 0; i < kW / 2; ++i) {
-        const uint32_t* rw = sm.red_u[g * (kW / 2) + i];
-        rg[g][0] = rw[0] < rg[g][0] ? rw[0] : rg[g][0];
-        rg[g][1] = rw[1] > rg[g][1] ? rw[1] : rg[g][1];
-        ntok += rw[2];
-        const int p = (int)(rw[3] & 0x3FFFu) - 1, n = (int)((rw[3] >> 14) & 0x3FFFu);
-        pm = p > pm ? p : pm;
-        nm = n < nm ? n : nm;
-        nesc |= rw[3] >> 28;
+      for (int o = 1; o < kW / 2; o <<= 1) {  // (within aligned groups of 8 lanes)
+        const uint32_t ol = (uint32_t)__shfl_xor((int)rlo, o, kWave);
+        const uint32_t oh = (uint32_t)__shfl_xor((int)rhi, o, kWave);
+        const int op = __shfl_xor(pm, o, kWave), on = __shfl_xor(nm, o, kWave);
+        nt += (uint32_t)__shfl_xor((int)nt, o, kWave);
+        es |= (uint32_t)__shfl_xor((int)es, o, kWave);
+        rlo = ol < rlo ? ol : rlo;
+        rhi = oh > rhi ? oh : rhi;
+        pm = op > pm ? op : pm;
+        nm = on < nm ? on : nm;
       }
-      // smallest value bin: the largest positive value, else the negative
-      // value nearest zero (bin v = kNI - 1 - i for the positive half of word
-      // i, kNI + i for the negative half)
-      top[g] = pm >= 0 ? kNI - 1u - (uint32_t)pm : (nm < (int)kNI ? kNI + (uint32_t)nm : (uint32_t)kNV);
-      // (an empty region: lo = hi = 0)
-      rg[g][0] = rg[g][1] ? rg[g][0] & ~3u : 0u;
-      rg[g][1] = (rg[g][1] + 3u) & ~3u;
+      const uint32_t nt_all = (uint32_t)__shfl((int)nt, 0, kWave) + (uint32_t)__shfl((int)nt, kW / 2, kWave);
+      const uint32_t es_all = (uint32_t)__shfl((int)es, 0, kWave) | (uint32_t)__shfl((int)es, kW / 2, kWave);
+      if (lane == 0 || lane == kW / 2) {
+        const int g = lane / (kW / 2);
+        // smallest value bin: the largest positive value, else the negative
+        // value nearest zero (bin v = kNI - 1 - i for the positive half of word
+        // i, kNI + i for the negative half); an empty region: lo = hi = 0
+        ex.pub[3 * g + 0] = rhi ? rlo & ~3u : 0u;
+        ex.pub[3 * g + 1] = (rhi + 3u) & ~3u;
+        ex.pub[3 * g + 2] =
+            pm >= 0 ? kNI - 1u - (uint32_t)pm : (nm < (int)kNI ? kNI + (uint32_t)nm : (uint32_t)kNV);
+      }
+      if (lane == 0) {
+        ex.pub[6] = nt_all;
+        ex.pub[7] = es_all;
+      }
     }
+    __syncthreads();
+    const uint32_t rg[2][2] = {{ex.pub[0], ex.pub[1]}, {ex.pub[3], ex.pub[4]}};
+    const uint32_t top[2] = {ex.pub[2], ex.pub[5]}, ntok = ex.pub[6], nesc = ex.pub[7];
     auto put = [&](uint32_t q) {  // u32x4 q of the bins to the slot, written through
       const u32x4 v = reinterpret_cast<const u32x4*>(sm.hist)[q];
       unsigned long long* d = reinterpret_cast<unsigned long long*>(slot) + 2 * q;
@@ -515,52 +530,7 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
   unsigned long long exw, W;
   uint32_t exc, N, N2;
   float lse_m, lse_s;
-  {
-    const unsigned long long iw = wave_scan_u64(Wt);
-    const uint32_t ic = wave_scan_u32(Nt);
-    const uint32_t s2 = wave_sum_u32(n2);
-    if (kMode == 2) wave_lse2(lm, lsum);
-    else if (kMode != 3) lsum = wave_sum_f(lsum);
-    __syncthreads();
-    if (lane == kWave - 1) {
-      sm.red_w[wid] = iw;
-      sm.red_u[wid][0] = ic;
-      sm.red_u[wid][1] = s2;
-      sm.red_f[wid][0] = lm;
-      sm.red_f[wid][1] = lsum;
-    }
-    __syncthreads();
-    unsigned long long bw = 0ull;
-    uint32_t bc = 0u;
-    W = 0ull;
-    N = N2 = 0u;
-    lse_m = kNegInf;
-#pragma unroll
-    for (int i = 0; i < kW; ++i) {
-      const unsigned long long vw = sm.red_w[i];
-      const uint32_t vc = sm.red_u[i][0];
-      if (i < wid) {
-        bw += vw;
-        bc += vc;
-      }
-      W += vw;
-      N += vc;
-      N2 += sm.red_u[i][1];
-      lse_m = sm.red_f[i][0] > lse_m ? sm.red_f[i][0] : lse_m;
-    }
-    lse_s = 0.0f;
-    if (kMode == 2) {
-#pragma unroll
-      for (int i = 0; i < kW; ++i)
-        if (sm.red_f[i][1] > 0.0f)
-          lse_s += sm.red_f[i][1] * __builtin_amdgcn_exp2f((sm.red_f[i][0] - lse_m) * kLog2e);
-    } else if (kMode != 3) {
-#pragma unroll
-      for (int i = 0; i < kW; ++i) lse_s += sm.red_f[i][1];
-    }
-    exw = bw + iw - Wt;
-    exc = bc + ic - Nt;
-  }
+  weight_scan<kMode>(sm, Wt, Nt, n2, lm, lsum, exw, exc, W, N, N2, lse_m, lse_s);
   if (!kPen && N + N2 != (uint32_t)V) return false;
   sm.x.ex.w[tid] = exw;
   sm.x.ex.c[tid] = exc;
