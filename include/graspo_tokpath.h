@@ -146,8 +146,13 @@ int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
  * gtp_sample_workspace_bytes -- workspace gtp_sample_rows needs for B rows of
  * V logits of `dtype` under `params` (0 when the call needs none).  Greedy and
  * top-k rows (1 <= top_k <= 128) split each row over several workgroups and
- * merge per-row candidate lists through the workspace; other calls run one
- * workgroup per row and need none.
+ * merge per-row candidate lists through the workspace.  Top-p rows without
+ * top-k at V >= 65536 (bf16, fp32) keep a hand-over list there, and bf16
+ * top-p batches of up to 64 rows also split each row over several
+ * workgroups, which merge their value counts through 64 KB slots (16.8 MB
+ * for 64 rows of 151936).  A smaller workspace, at least the hand-over
+ * list's (B + 2) * 4 bytes rounded up to 256, gives those top-p calls fewer
+ * slices or one workgroup per row; other calls need none.
  */
 size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                   const gtp_sampler_params* params);
