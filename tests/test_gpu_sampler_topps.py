@@ -7,7 +7,8 @@ Covers every (penalty, mask) variant on small batches and vocabulary tails
 several slices (the wanted token's slice and its rank there come from the
 slices' counts), the cut and the draw in different slices, a value held by
 more than 65535 tokens of a row but fewer in each slice (the merged 16-bit
-count overflows: the row is handed over), a value outside the bins in one
+count overflows: the row is handed over) or 65536 times in one slice (that
+slice's count wraps: its token total gives it away), a value outside the bins in one
 slice only, status rows, and the no-allocation entry point, whose 8 MiB
 array holds fewer slices."""
 
@@ -132,3 +133,18 @@ def test_noalloc_entry_point_uses_fewer_slices():
     assert np.array_equal(got["ids"].numpy(), ref.ids)
     assert np.array_equal(got["kept"].numpy(), ref.kept)
     assert np.array_equal(got["thresh_id"].numpy(), ref.thresh_id)
+
+
+def test_slice_count_overflow():
+    """[64, 262144]: 4 slices of 65536 tokens.  Row 0's first slice holds one
+    value 65536 times, so that slice's 16-bit count wraps; the slice's token
+    total no longer adds up and the row is handed over.  Row 1 holds the
+    value 40000 times in each of two slices (80000 in the row)."""
+    B, V = 64, 262144
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B, V, generator=g) * 2
+    x[0, :65536] = 1.5
+    x[1, 10000:50000] = 1.5
+    x[1, 70000:110000] = 1.5
+    x = x.to(torch.bfloat16)
+    _check(x, "slice count overflow", temperature=1.0, top_p=0.9, uniforms=_u(B, g))
