@@ -171,8 +171,10 @@ size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
  * GTP_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
  * process ends; the first call on a device looks up that device's copy.
  * Each call first clears the array's per-row counters with a small fill
- * kernel on `stream`.  Returns GTP_ERR_UNSUPPORTED when the call needs more
- * than GTP_NOALLOC_SCRATCH_BYTES (gtp_sample_workspace_bytes() tells), e.g.
+ * kernel on `stream`.  bf16 top-p calls of small batches, whose split rows
+ * would need more, split their rows over fewer workgroups (or none) to fit.
+ * Returns GTP_ERR_UNSUPPORTED when any other call needs more than
+ * GTP_NOALLOC_SCRATCH_BYTES (gtp_sample_workspace_bytes() tells), e.g.
  * thousands of fp32 rows of a 2^18 vocabulary.  Every call on one GPU shares
  * that GPU's array: calls that may overlap on one GPU (different streams,
  * host threads) race and must be serialised by the caller.
