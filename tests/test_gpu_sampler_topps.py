@@ -148,3 +148,25 @@ def test_slice_count_overflow():
     x[1, 70000:110000] = 1.5
     x = x.to(torch.bfloat16)
     _check(x, "slice count overflow", temperature=1.0, top_p=0.9, uniforms=_u(B, g))
+
+
+def test_repeated_calls_agree_with_the_one_workgroup_kernel():
+    """40 back-to-back calls on fresh rows of one shape (the workspace's
+    slots hold the previous call's counts): every split result equals the
+    one-workgroup kernel's bit for bit, so no merge read a stale slot."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    B, V = 48, 151936
+    hist = torch.randint(0, V, (B, 512), generator=g, device=dev, dtype=torch.int32)
+    for it in range(40):
+        x = (torch.randn(B, V, generator=g, device=dev) * (1.5 + (it % 5))).to(torch.bfloat16)
+        u = torch.randint(0, 1 << 24, (B,), generator=g, device=dev).float() * 2.0 ** -24
+        kw = dict(temperature=0.6 + 0.1 * (it % 7), top_p=0.8 + 0.04 * (it % 5), uniforms=u)
+        if it % 2:
+            kw.update(history=hist, repetition_penalty=1.15)
+        got = gpu_sample(x, **kw)
+        one = one_workgroup_sample(x, **kw)
+        for f in ("ids", "kept", "thresh_id", "status"):
+            assert torch.equal(getattr(got, f), getattr(one, f)), (it, f)
+        assert torch.equal(got.thresh_value.view(torch.int32), one.thresh_value.view(torch.int32)), it
+        assert torch.equal(got.sampled_logprob.view(torch.int32), one.sampled_logprob.view(torch.int32)), it
