@@ -233,9 +233,11 @@ def sample_semantic(
 ):
     """Literal fp64 restatement of tensor_utils.py:649-683 (+ contract extensions).
 
-    Returns per row (id, kept, cut_margin, draw_margin): the margins are the
-    distance of the top-p comparison and of the uniform from the nearest
-    decision boundary, so callers can tell near-ties from disagreements."""
+    Returns per row (id, kept, cut_margin, draw_margin, p_sampled): the
+    margins are the distance of the top-p comparison and of the uniform from
+    the nearest decision boundary, so callers can tell near-ties from
+    disagreements; p_sampled is the drawn token's probability in the
+    renormalised kept set (tensor_utils.py:679-683), 1 for greedy rows."""
     import torch
 
     x = np.asarray(x, dtype=np.float32)
@@ -250,13 +252,13 @@ def sample_semantic(
         else:
             allow = torch.from_numpy(allowed[b])
             if not bool(allow.any()):
-                out.append((-1, 0, np.inf, np.inf))
+                out.append((-1, 0, np.inf, np.inf, np.nan))
                 continue
             masked = torch.where(allow, row, torch.tensor(-np.inf))
             gid = int(torch.argmax(masked))  # tensor_utils.py:658 (NaN, then +inf, win)
             if not bool(allow[gid]):  # every allowed token is -inf: the first of them
                 gid = int(allow.nonzero()[0])
-            out.append((gid, 1, np.inf, np.inf))
+            out.append((gid, 1, np.inf, np.inf, 1.0))
             continue
         y = row.double()
         y = torch.where(torch.from_numpy(allowed[b]), y, torch.tensor(-np.inf, dtype=torch.float64))
@@ -281,7 +283,7 @@ def sample_semantic(
         r = int(torch.searchsorted(cdf, torch.tensor([u], dtype=torch.float64), right=True)[0])
         r = min(r, R - 1)
         draw_margin = float((cdf - u).abs().min())
-        out.append((int(idx[r]), R, cut_margin, draw_margin))
+        out.append((int(idx[r]), R, cut_margin, draw_margin, float(kept[r])))
     return out
 
 

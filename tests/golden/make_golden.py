@@ -16,6 +16,8 @@ not from this repository's oracle:
 * draw: inverse CDF of the supplied uniform over the renormalised kept set in
   fp64 (the reference calls ``torch.multinomial``; the contract replaces its
   global-RNG draw by a supplied uniform);
+* sampled logprob: ``log`` of the drawn token's fp64 probability in that
+  renormalised kept set (tensor_utils.py:679-683), 0 for greedy rows;
 * logprob / entropy: ``torch.log_softmax`` in fp64.
 
 Uniforms are moved, and top-p values chosen, so that every fp64 cumulative
@@ -54,8 +56,8 @@ def pack_bits(bits: np.ndarray) -> np.ndarray:
 
 
 def expected_row(x: torch.Tensor, hist, rho, allowed, T, k, P, u):
-    """(id, kept, thresh_value, thresh_id, logprob, u_used) of one row, or
-    None when a top-p boundary lies within MARGIN of P."""
+    """(id, kept, thresh_value, thresh_id, logprob, sampled_logprob, u_used)
+    of one row, or None when a top-p boundary lies within MARGIN of P."""
     V = x.numel()
     xp = x.clone()
     if hist is not None and rho != 1.0:
@@ -67,7 +69,7 @@ def expected_row(x: torch.Tensor, hist, rho, allowed, T, k, P, u):
     lsm = torch.log_softmax(x.double(), 0)
     if not (T > 0):
         i = int(torch.argmax(xp))
-        return i, 1, float(xp[i]), i, float(lsm[i]), u
+        return i, 1, float(xp[i]), i, float(lsm[i]), 0.0, u
     y = xp / max(T, 1e-6)  # one IEEE fp32 division
     ys, order = torch.sort(y, descending=True, stable=True)
     n_valid = int(torch.isfinite(ys).sum())
@@ -89,7 +91,8 @@ def expected_row(x: torch.Tensor, hist, rho, allowed, T, k, P, u):
         u = float(np.float32(u + 2.0 ** -12)) % 1.0
     r = int((cum <= u).sum())
     i = int(order[r])
-    return i, int(order.numel()), float(ys[-1]), int(order[-1]), float(lsm[i]), u
+    return (i, int(order.numel()), float(ys[-1]), int(order[-1]), float(lsm[i]),
+            float(torch.log(p[r])), u)
 
 
 def sampler_case(name, seed, B, V, *, scale, T, k, P, rho=1.0, hist_len=0, density=None,
@@ -109,7 +112,8 @@ def sampler_case(name, seed, B, V, *, scale, T, k, P, rho=1.0, hist_len=0, densi
         allowed[-1] = False
         allowed[-1, int(rng.integers(0, V))] = True  # one row with a single allowed token
     u = (rng.integers(0, 1 << 24, B) * 2.0 ** -24).astype(np.float32)
-    exp = {n: [] for n in ("ids", "kept", "thresh_value", "thresh_id", "logprob")}
+    exp = {n: [] for n in ("ids", "kept", "thresh_value", "thresh_id", "logprob",
+                           "sampled_logprob")}
     for b in range(B):
         r = None
         while r is None:
@@ -119,9 +123,9 @@ def sampler_case(name, seed, B, V, *, scale, T, k, P, rho=1.0, hist_len=0, densi
                 j = int(torch.argmax(xv[b]))
                 bits[b, j] += 1
                 xv[b] = bf16_values(bits[b : b + 1])[0]
-        i, kept, tv, tid, lp, u_used = r
+        i, kept, tv, tid, lp, slp, u_used = r
         u[b] = u_used
-        for n, v in zip(exp, (i, kept, tv, tid, lp)):
+        for n, v in zip(exp, (i, kept, tv, tid, lp, slp)):
             exp[n].append(v)
     arrays = dict(
         logits_bf16=bits, V=np.int64(V), temperature=np.float32(T), top_k=np.int32(k),
@@ -130,6 +134,7 @@ def sampler_case(name, seed, B, V, *, scale, T, k, P, rho=1.0, hist_len=0, densi
         exp_thresh_value=np.array(exp["thresh_value"], np.float32),
         exp_thresh_id=np.array(exp["thresh_id"], np.int32),
         exp_logprob=np.array(exp["logprob"], np.float64),
+        exp_sampled_logprob=np.array(exp["sampled_logprob"], np.float64),
     )
     if hist is not None:
         arrays["history"] = hist

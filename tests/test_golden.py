@@ -1,7 +1,9 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py
 from transformers' repetition-penalty processor, torch's stable sort, the
 reference's top-p rule in fp64 and torch.log_softmax in fp64) against the CPU
-oracle and against the gfx950 kernels."""
+oracle and against the gfx950 kernels.  Each sampler fixture also holds the
+fp64 log of the drawn token's renormalised probability, which pins the
+contract's sampled_logprob = log(w / W') independently of the oracle."""
 
 import glob
 import os
@@ -30,7 +32,7 @@ def _sampler_kwargs(f):
                 uniforms=f["uniforms"])
 
 
-def _check_sampler(name, f, ids, kept, tv, tid, lp, status):
+def _check_sampler(name, f, ids, kept, tv, tid, lp, slp, status):
     assert (status == 0).all(), f"{name}: status {status}"
     np.testing.assert_array_equal(ids, f["exp_ids"], err_msg=f"{name}: ids")
     np.testing.assert_array_equal(kept, f["exp_kept"], err_msg=f"{name}: kept")
@@ -38,6 +40,8 @@ def _check_sampler(name, f, ids, kept, tv, tid, lp, status):
     np.testing.assert_array_equal(tv.view(np.uint32), f["exp_thresh_value"].view(np.uint32),
                                   err_msg=f"{name}: threshold value")
     assert np.abs(lp.astype(np.float64) - f["exp_logprob"]).max() <= LP_TOL, f"{name}: logprob"
+    assert np.abs(slp.astype(np.float64) - f["exp_sampled_logprob"]).max() <= LP_TOL, (
+        f"{name}: sampled logprob")
 
 
 def test_fixtures_present():
@@ -49,7 +53,7 @@ def test_oracle_matches_sampler_fixture(path):
     f = _load(path)
     r = O.sample_rows(f["logits_bf16"], O.DTYPE_BF16, **_sampler_kwargs(f))
     _check_sampler(os.path.basename(path), f, r.ids, r.kept, r.thresh_value, r.thresh_id,
-                   r.logprob, r.status)
+                   r.logprob, r.sampled_logprob, r.status)
 
 
 @pytest.mark.parametrize("path", LOGPROB, ids=lambda p: os.path.basename(p)[:-4])
@@ -85,7 +89,8 @@ def test_gpu_matches_sampler_fixture(path):
     torch.cuda.synchronize()
     _check_sampler(os.path.basename(path), f, out.ids.cpu().numpy(), out.kept.cpu().numpy(),
                    out.thresh_value.cpu().numpy(), out.thresh_id.cpu().numpy(),
-                   out.logprob.cpu().numpy(), out.status.cpu().numpy())
+                   out.logprob.cpu().numpy(), out.sampled_logprob.cpu().numpy(),
+                   out.status.cpu().numpy())
 
 
 @pytest.mark.gpu

@@ -35,12 +35,23 @@ def test_exact_oracle_matches_semantic_restatement(cfg, rows):
     ex = oracle_sample(wl.logits, **wl.kwargs())
     sem = _sem(wl)
     assert (ex.status == O.ROW_OK).all()
-    for b, (sid, skept, cut_margin, draw_margin) in enumerate(sem):
+    compared = 0
+    for b, (sid, skept, cut_margin, draw_margin, p_sampled) in enumerate(sem):
         if ex.ids[b] != sid or ex.kept[b] != skept:
             # only a measured near-tie may separate fixed point from fp64
             assert min(cut_margin, draw_margin) < 1e-9, (b, ex.ids[b], sid, ex.kept[b], skept)
+            continue
+        # sampled_logprob is log of the drawn token's probability in the
+        # renormalised kept set (tensor_utils.py:679-683), evaluated here by
+        # torch's fp64 softmax over the kept ranks: an independent pin of the
+        # oracle's log(w / W') (a W in place of W' is off by -log(mass kept))
+        assert abs(float(ex.sampled_logprob[b]) - math.log(p_sampled)) <= 1e-4, (
+            b, float(ex.sampled_logprob[b]), math.log(p_sampled))
+        compared += 1
+    assert compared >= rows - 2
     for r, t in wl.single_rows.items():
         assert ex.ids[r] == t and ex.kept[r] == 1
+        assert ex.sampled_logprob[r] == 0.0
 
 
 def _exact_probs(y: np.ndarray, top_k: int, top_p: float):
@@ -75,6 +86,10 @@ def test_tiny_rows_exhaustive_uniform_grid(seed):
     assert set(r.kept.tolist()) == {len(order)}
     freq = np.array([(r.ids == i).sum() / n for i in order])
     assert np.abs(freq - p).max() <= 1.0 / n + 1e-6
+    # each draw reports log of its token's exact renormalised probability
+    prob = dict(zip(order, p))
+    want_lp = np.array([math.log(prob[i]) for i in r.ids])
+    assert np.abs(r.sampled_logprob.astype(np.float64) - want_lp).max() <= 1e-5
     assert set(r.ids.tolist()) <= set(order)
     # monotone in u: ranks never go back
     rank = {t: k for k, t in enumerate(order)}
