@@ -2,15 +2,21 @@
 TEST / MEASUREMENT INFRASTRUCTURE ONLY (never imported by graspo_amd).
 
 A literal torch restatement of what the reference runs per decode step and
-per loss step, on CPU tensors:
+per loss step, on CPU tensors, in the reference's fp32:
 
 * sampler: tensor_utils.py:649-683 (``logits / max(T, 1e-6)``, softmax,
   descending sort, cumsum, shifted ``cum > top_p`` cut, renormalise, draw),
-  with the contract's extensions applied first (HF-style repetition penalty,
-  allow mask, top-k) and ``torch.multinomial`` replaced by the inverse CDF of
-  the supplied uniform;
+  with the contract's extensions applied first (HF-style repetition penalty
+  over the row's history ids, negative ids being padding; allow mask; top-k
+  keeping exactly k tokens in (y desc, id asc) order) and
+  ``torch.multinomial`` replaced by the inverse CDF of the supplied uniform;
 * logprob: graspo_loss.py:19-21 (``log_softmax`` then ``gather``) plus the
   entropy of the same log-softmax.
+
+The one sort of a row is stable and descending, so ties are ordered by
+ascending id as the contract orders them; the reference's sort of the
+softmax probabilities leaves equal probabilities in an unspecified order,
+which only changes which of two equally likely tokens a uniform lands on.
 """
 
 from __future__ import annotations
@@ -18,24 +24,32 @@ from __future__ import annotations
 import torch
 
 
+def penalised(x, history, repetition_penalty):
+    """HF's ``RepetitionPenaltyLogitsProcessor`` rule (x < 0 ? x*rho : x/rho)
+    once per distinct history id of each row; ids < 0 are padding and
+    penalise nothing."""
+    h = history.long()
+    valid = (h >= 0) & (h < x.shape[1])
+    hits = torch.zeros(x.shape, dtype=torch.int32)
+    hits.scatter_add_(1, torch.where(valid, h, 0), valid.to(torch.int32))
+    pen = torch.where(x < 0, x * repetition_penalty, x / repetition_penalty)
+    return torch.where(hits > 0, pen, x)
+
+
 def sample_rows(logits, *, temperature, top_k=0, top_p=1.0, repetition_penalty=1.0,
                 history=None, allow_mask_bits=None, uniforms=None):
     x = logits.float()
     if history is not None and repetition_penalty != 1.0:
-        h = history.long().clamp_min(0)
-        vals = x.gather(1, h)
-        vals = torch.where(vals < 0, vals * repetition_penalty, vals / repetition_penalty)
-        x = x.scatter(1, h, vals)
+        x = penalised(x, history, repetition_penalty)
     if allow_mask_bits is not None:
         x = x.masked_fill(~allow_mask_bits, float("-inf"))
     if temperature <= 0:
         return x.argmax(dim=-1)
     x = x / max(float(temperature), 1e-6)
+    ys, sorted_idx = torch.sort(x, dim=-1, descending=True, stable=True)
     if top_k > 0:
-        kth = torch.topk(x, top_k, dim=-1).values[:, -1:]
-        x = x.masked_fill(x < kth, float("-inf"))
-    probs = torch.softmax(x, dim=-1)
-    sorted_probs, sorted_idx = torch.sort(probs, descending=True, dim=-1)
+        ys[:, top_k:] = float("-inf")
+    sorted_probs = torch.softmax(ys, dim=-1)
     if 0.0 < top_p < 1.0:
         cum = torch.cumsum(sorted_probs, dim=-1)
         remove = cum > top_p
@@ -44,8 +58,10 @@ def sample_rows(logits, *, temperature, top_k=0, top_p=1.0, repetition_penalty=1
         sorted_probs = sorted_probs.masked_fill(remove, 0.0)
     sorted_probs = sorted_probs / sorted_probs.sum(dim=-1, keepdim=True).clamp_min(1e-12)
     cdf = torch.cumsum(sorted_probs, dim=-1)
-    r = torch.searchsorted(cdf, uniforms.float().unsqueeze(1), right=True).clamp_max(
-        cdf.shape[1] - 1)
+    r = torch.searchsorted(cdf, uniforms.float().unsqueeze(1), right=True)
+    # the last kept rank takes a uniform beyond the rounded cdf total
+    kept = (sorted_probs > 0).sum(dim=-1, keepdim=True)
+    r = torch.minimum(r, kept - 1)
     return sorted_idx.gather(1, r).squeeze(1)
 
 
