@@ -69,6 +69,8 @@ struct Args {
   int64_t V, N, K, ldw, ldh;
   int n_vfull, n_tt, n_vg;  // full vocabulary tiles, token tiles, groups of full tiles
   float4* partial;          // [2 * n_vg + 2][N]: (m, s, t, 0), t in base-2 units
+  float* logits;            // [V, N] fp32, vocabulary-major, row stride ldl (kStore only)
+  int64_t ldl;
 };
 
 // s_waitcnt vmcnt(0), the other counters untouched
@@ -103,7 +105,14 @@ __device__ __forceinline__ float swap_halves(float v) {
 // kTail = false: the full vocabulary tiles, kTilesPerGroup per workgroup.
 // kTail = true: the last, partial tile (V mod 256 rows), one per token tile,
 // its rows past V masked in the epilogue; its partials follow the groups'.
-template <bool kTail>
+// kStore: the epilogue also writes every logit of the tile to a.logits,
+// vocabulary-major: one non-temporal dword store per value, whose 32 lanes of
+// a lane half hold 32 consecutive tokens of one vocabulary row, so that each
+// store instruction writes two whole 128-byte lines (rows past V and tokens
+// past N are not written).  Token-major 16-byte stores (4 rows of a token
+// per lane, 32 bytes per token row per instruction) cost 4.2 ms on top of
+// the 13.5 ms GEMM at 8192 x 4096 x 248320.
+template <bool kTail, bool kStore>
 __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) uint4 sA0[kStage], sA1[kStage], sB0[kStage], sB1[kStage];
 
@@ -261,10 +270,10 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     int lim = 128;  // valid row offsets of this lane half are < lim
-    if constexpr (kTail) {
-      const int64_t vb = (int64_t)(vt0 + tile) * kBV + wv * 128 + 4 * (lane >> 5);
-      lim = (int)min((int64_t)128, max(a.V - vb, (int64_t)0));
-    }
+    // first vocabulary row of this lane half's values: value i of block x is
+    // row vb + 32 x + 8 (i >> 2) + (i & 3)
+    const int64_t vb = (int64_t)(vt0 + tile) * kBV + wv * 128 + 4 * (lane >> 5);
+    if constexpr (kTail) lim = (int)min((int64_t)128, max(a.V - vb, (int64_t)0));
 #pragma unroll 1
     for (int r = 0; r < kYB; ++r) {
       float m = kNegInf, s = 0.0f, t = 0.0f;
@@ -272,9 +281,27 @@ __global__ __launch_bounds__(kThreads, 1) void lm_head_lse_kernel(Args a) {
       for (int x = 0; x < kXB; ++x) {
         float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          v[i] = acc_read(acc[x][0][i]);
-          if constexpr (kTail)
+        for (int i = 0; i < 16; ++i) v[i] = acc_read(acc[x][0][i]);
+        if constexpr (kStore) {
+          // this trip folds token block r: token (lane & 31) of it
+          const int64_t n = (int64_t)tt * kBT + wt * (kYB * 32) + r * 32 + (lane & 31);
+          if (n < a.N) {
+            // one running address, stepped through rows 0-3, 8-11, 16-19,
+            // 24-27 of the block (the empty asm keeps the compiler from
+            // holding all 16 addresses in registers across the tile loop)
+            const int64_t ld = a.ldl;
+            float* p = a.logits + (vb + x * 32) * ld + n;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              if (!kTail || x * 32 + 8 * (i >> 2) + (i & 3) < lim) __builtin_nontemporal_store(v[i], p);
+              p += (i & 3) == 3 ? 5 * ld : ld;
+              asm volatile("" : "+v"(p));
+            }
+          }
+        }
+        if constexpr (kTail) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
             if (x * 32 + 8 * (i >> 2) + (i & 3) >= lim) v[i] = kNegInf;
         }
         float cm = v[0];
@@ -445,12 +472,14 @@ extern "C" size_t gtp_lm_head_workspace_bytes(int64_t N, int64_t V) {
   return p.partial_bytes + p.xt_bytes;
 }
 
-extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64_t K,
-                                        int64_t hidden_stride, const uint16_t* weight, int64_t V,
-                                        int64_t weight_stride, const void* targets,
-                                        int targets_int64, float* out_logprob, float* out_entropy,
-                                        float* out_lse, int32_t* out_status, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+namespace {
+// Both entry points: out_logits == nullptr runs the kernels that write no
+// logits.
+int lm_head_run(const uint16_t* hidden, int64_t N, int64_t K, int64_t hidden_stride,
+                const uint16_t* weight, int64_t V, int64_t weight_stride, const void* targets,
+                int targets_int64, float* out_logprob, float* out_entropy, float* out_lse,
+                int32_t* out_status, float* out_logits, int64_t logits_stride, void* workspace,
+                size_t workspace_bytes, void* stream) {
   if (N < 0 || V <= 0 || K <= 0 || hidden_stride < K || weight_stride < K ||
       (N > 0 && (!hidden || !weight || !targets || !out_logprob || !workspace)))
     return GTP_ERR_INVALID_ARGUMENT;
@@ -460,6 +489,11 @@ extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64
       hidden_stride > lmh::kMaxLd || weight_stride > lmh::kMaxLd ||
       (reinterpret_cast<uintptr_t>(hidden) & 15u) || (reinterpret_cast<uintptr_t>(weight) & 15u))
     return GTP_ERR_UNSUPPORTED;
+  if (out_logits) {
+    if (logits_stride < N) return GTP_ERR_INVALID_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(out_logits) & 3u) || logits_stride > ((int64_t)1 << 40) / V)
+      return GTP_ERR_UNSUPPORTED;
+  }
   if (N == 0) return GTP_OK;
   const lmh::Plan p = lmh::plan(N, V);
   if (workspace_bytes < p.partial_bytes + p.xt_bytes) return GTP_ERR_INVALID_ARGUMENT;
@@ -476,13 +510,24 @@ extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64
   a.n_tt = p.n_tt;
   a.n_vg = p.n_vg;
   a.partial = reinterpret_cast<float4*>(workspace);
+  a.logits = out_logits;
+  a.ldl = logits_stride;
   float* xt = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + p.partial_bytes);
   const int64_t grid = (int64_t)p.n_vg * p.n_tt;
   if (grid > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
-  if (grid > 0) launch_timed(lmh::lm_head_lse_kernel<false>, dim3((unsigned)grid), dim3(lmh::kThreads), s, a);
-  if (p.tail)
-    hipLaunchKernelGGL(lmh::lm_head_lse_kernel<true>, dim3((unsigned)p.n_tt), dim3(lmh::kThreads), 0,
-                       s, a);
+  if (out_logits) {
+    if (grid > 0)
+      launch_timed(lmh::lm_head_lse_kernel<false, true>, dim3((unsigned)grid), dim3(lmh::kThreads), s, a);
+    if (p.tail)
+      hipLaunchKernelGGL((lmh::lm_head_lse_kernel<true, true>), dim3((unsigned)p.n_tt),
+                         dim3(lmh::kThreads), 0, s, a);
+  } else {
+    if (grid > 0)
+      launch_timed(lmh::lm_head_lse_kernel<false, false>, dim3((unsigned)grid), dim3(lmh::kThreads), s, a);
+    if (p.tail)
+      hipLaunchKernelGGL((lmh::lm_head_lse_kernel<true, false>), dim3((unsigned)p.n_tt),
+                         dim3(lmh::kThreads), 0, s, a);
+  }
   hipLaunchKernelGGL(lmh::lm_head_target_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s,
                      weight, hidden, N, V, K, weight_stride, hidden_stride, targets, targets_int64,
                      xt);
@@ -491,4 +536,32 @@ extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64
                      a.partial, 2 * p.n_vg + (p.tail ? 2 : 0), N, xt, out_logprob, out_entropy,
                      out_lse, out_status);
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+}
+}  // namespace
+
+extern "C" int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64_t K,
+                                        int64_t hidden_stride, const uint16_t* weight, int64_t V,
+                                        int64_t weight_stride, const void* targets,
+                                        int targets_int64, float* out_logprob, float* out_entropy,
+                                        float* out_lse, int32_t* out_status, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return lm_head_run(hidden, N, K, hidden_stride, weight, V, weight_stride, targets,
+                     targets_int64, out_logprob, out_entropy, out_lse, out_status, nullptr, 0,
+                     workspace, workspace_bytes, stream);
+}
+
+extern "C" int gtp_lm_head_logprob_save_rows(const uint16_t* hidden, int64_t N, int64_t K,
+                                             int64_t hidden_stride, const uint16_t* weight,
+                                             int64_t V, int64_t weight_stride,
+                                             const void* targets, int targets_int64,
+                                             float* out_logprob, float* out_entropy,
+                                             float* out_lse, int32_t* out_status,
+                                             float* out_logits, int64_t logits_stride,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  if (N > 0 && !out_logits) return GTP_ERR_INVALID_ARGUMENT;
+  return lm_head_run(hidden, N, K, hidden_stride, weight, V, weight_stride, targets,
+                     targets_int64, out_logprob, out_entropy, out_lse, out_status,
+                     N > 0 ? out_logits : nullptr, logits_stride, workspace, workspace_bytes,
+                     stream);
 }

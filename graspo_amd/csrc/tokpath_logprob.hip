@@ -450,6 +450,78 @@ extern "C" int gtp_logprob_backward_split_rows(const float* logits, int64_t N, i
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }
 
+// bf16(-g_n p) of vocabulary-major fp32 logits, p = exp(x_t[v, n] - lse_n):
+// the softmax part of g_n ([v == t_n] - p) without the one-hot term, which
+// the caller adds in fp32 (it is the one term of a token's gradient near g
+// in size; here every element is g p, rounded once to bf16, within 2^-8 of
+// it).  A workgroup takes 1024 consecutive tokens (4 per thread, their g and
+// lse held in registers) of kSgRows vocabulary rows; a token with g == 0
+// gets zeros.
+constexpr int kSgRows = 16;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void softmax_grad_bf16_cols_kernel(
+    const float* __restrict__ logits_t, int64_t V, int64_t N, int64_t ld,
+    const float* __restrict__ grad_lp, const float* __restrict__ lse_in,
+    uint16_t* __restrict__ grad_t, int64_t gld, int vec) {
+  const int64_t n0 = (int64_t)blockIdx.x * 1024 + threadIdx.x * 4;
+  if (n0 >= N) return;
+  const int64_t v0 = (int64_t)blockIdx.y * kSgRows;
+  const int cnt = (int)min((int64_t)4, N - n0);
+  float ng[4], c[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float g = j < cnt ? grad_lp[n0 + j] : 0.0f;
+    ng[j] = -g;
+    // a token with g == 0 gets exactly zero
+    c[j] = g == 0.0f ? kNegInf : (j < cnt ? lse_in[n0 + j] : 0.0f);
+  }
+  // x - lse first: exact for x near lse at any magnitude
+  auto grad_of = [&](float x, int j) {
+    return c[j] == kNegInf ? 0.0f : ng[j] * __builtin_amdgcn_exp2f((x - c[j]) * kLog2e);
+  };
+  if (vec && cnt == 4) {
+#pragma unroll 4
+    for (int r = 0; r < kSgRows; ++r) {
+      const int64_t v = v0 + r;
+      if (v >= V) break;
+      const f32x4v x = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(logits_t + v * ld + n0));
+      const u32x2 o = {bf16_rne(grad_of(x.x, 0)) | (bf16_rne(grad_of(x.y, 1)) << 16),
+                       bf16_rne(grad_of(x.z, 2)) | (bf16_rne(grad_of(x.w, 3)) << 16)};
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(grad_t + v * gld + n0));
+    }
+    return;
+  }
+  for (int r = 0; r < kSgRows; ++r) {
+    const int64_t v = v0 + r;
+    if (v >= V) break;
+    for (int j = 0; j < cnt; ++j)
+      grad_t[v * gld + n0 + j] = (uint16_t)bf16_rne(grad_of(logits_t[v * ld + n0 + j], j));
+  }
+}
+
+extern "C" int gtp_softmax_grad_bf16_cols(const float* logits_t, int64_t V, int64_t N,
+                                          int64_t logits_stride, const float* grad_logprob,
+                                          const float* lse, uint16_t* grad_t, int64_t grad_stride,
+                                          void* stream) {
+  if (N < 0 || V <= 0 || logits_stride < N || grad_stride < N ||
+      (N > 0 && (!logits_t || !grad_logprob || !lse || !grad_t)))
+    return GTP_ERR_INVALID_ARGUMENT;
+  if (N > 0x7FFFFFFFll || V > ((int64_t)65535 * kSgRows) ||
+      logits_stride > ((int64_t)1 << 40) / V || grad_stride > ((int64_t)1 << 40) / V)
+    return GTP_ERR_UNSUPPORTED;
+  if (N == 0) return GTP_OK;
+  const int vec = ((reinterpret_cast<uintptr_t>(logits_t) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(grad_t) & 7u) == 0 && (logits_stride & 3) == 0 &&
+                   (grad_stride & 3) == 0)
+                      ? 1
+                      : 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((N + 1023) / 1024), (unsigned)((V + kSgRows - 1) / kSgRows));
+  launch_timed(softmax_grad_bf16_cols_kernel, grid, dim3(256), s, logits_t, V, N, logits_stride,
+               grad_logprob, lse, grad_t, grad_stride, vec);
+  return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
+}
+
 extern "C" int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N, int64_t V,
                                          int64_t row_stride, int64_t col_offset,
                                          const void* targets, int targets_int64,

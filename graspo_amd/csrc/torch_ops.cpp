@@ -2,7 +2,7 @@
 //
 // Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
 // lse_finalize, decode_update, to_bf16_exact, logprob_backward_split, time_next_launch,
-// lm_head_logprob}.  Each op validates its tensors (TORCH_CHECK surfaces as a
+// lm_head_logprob, lm_head_logprob_save, softmax_grad_bf16}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
 // enqueues the HIP kernels on the stream handle passed in from Python
 // (torch.cuda.current_stream().cuda_stream), so work orders with the
@@ -467,6 +467,66 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> lm_head_logprob(const at::Tensor&
   return {lp, H, lse};
 }
 
+// lm_head_logprob that also keeps the fp32 logits, vocabulary-major [V, N],
+// and returns the per-row status, for the backward.
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> lm_head_logprob_save(
+    const at::Tensor& hidden, const at::Tensor& weight, const at::Tensor& targets,
+    int64_t stream) {
+  for (const at::Tensor* t : {&hidden, &weight}) {
+    TORCH_CHECK(t->is_cuda(),
+                "graspo_tokpath.lm_head_logprob_save: hidden / weight must be GPU tensors");
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16 && t->dim() == 2 && t->stride(1) == 1,
+                "graspo_tokpath.lm_head_logprob_save: hidden / weight must be bfloat16 2-D "
+                "with contiguous rows");
+  }
+  check_same_device(hidden, weight, "weight");
+  const int64_t N = hidden.size(0), K = hidden.size(1), V = weight.size(0);
+  TORCH_CHECK(weight.size(1) == K, "graspo_tokpath.lm_head_logprob_save: hidden is [N, ", K,
+              "] but weight is [V, ", weight.size(1), "]");
+  int t64 = 0;
+  const void* tp = targets_ptr(hidden, targets, N, &t64);
+  at::Tensor lp = at::empty({N}, hidden.options().dtype(at::kFloat));
+  at::Tensor lse = at::empty({N}, lp.options());
+  at::Tensor status = at::empty({N}, lp.options().dtype(at::kInt));
+  at::Tensor logits_t = at::empty({V, N}, lp.options());
+  const size_t ws_bytes = gtp_lm_head_workspace_bytes(N, V);
+  at::Tensor ws = at::empty({(int64_t)ws_bytes}, hidden.options().dtype(at::kByte));
+  const int64_t ldh = N > 1 ? hidden.stride(0) : K, ldw = V > 1 ? weight.stride(0) : K;
+  const int rc = gtp_lm_head_logprob_save_rows(
+      reinterpret_cast<const uint16_t*>(hidden.data_ptr()), N, K, ldh,
+      reinterpret_cast<const uint16_t*>(weight.data_ptr()), V, ldw, tp, t64, lp.data_ptr<float>(),
+      nullptr, lse.data_ptr<float>(), status.data_ptr<int32_t>(), logits_t.data_ptr<float>(),
+      N, ws.data_ptr(), ws_bytes, reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_lm_head_logprob_save_rows");
+  return {lp, lse, logits_t, status};
+}
+
+// bf16(-g * softmax) of vocabulary-major fp32 logits [V, N] (row stride
+// free, unit column stride), g and lse fp32 [N]; returns [V, N] bf16
+at::Tensor softmax_grad_bf16(const at::Tensor& logits_t, const at::Tensor& grad_logprob,
+                             const at::Tensor& lse, int64_t stream) {
+  TORCH_CHECK(logits_t.is_cuda() && logits_t.scalar_type() == at::kFloat && logits_t.dim() == 2 &&
+                  (logits_t.size(1) <= 1 || logits_t.stride(1) == 1),
+              "graspo_tokpath.softmax_grad_bf16: logits_t must be a float32 [V, N] GPU tensor "
+              "with unit column stride");
+  const int64_t V = logits_t.size(0), N = logits_t.size(1);
+  check_same_device(logits_t, grad_logprob, "grad_logprob");
+  check_same_device(logits_t, lse, "lse");
+  TORCH_CHECK(grad_logprob.scalar_type() == at::kFloat && grad_logprob.numel() == N &&
+                  grad_logprob.is_contiguous() && lse.scalar_type() == at::kFloat &&
+                  lse.numel() == N && lse.is_contiguous(),
+              "graspo_tokpath.softmax_grad_bf16: grad_logprob and lse must be float32 [N]");
+  at::Tensor out = at::empty({V, N}, logits_t.options().dtype(at::kBFloat16));
+  if (V == 0 || N == 0) return out;
+  const int64_t ld = V > 1 ? logits_t.stride(0) : N;
+  const int rc = gtp_softmax_grad_bf16_cols(
+      logits_t.data_ptr<float>(), V, N, ld, grad_logprob.data_ptr<float>(),
+      lse.data_ptr<float>(), static_cast<uint16_t*>(out.data_ptr()), N,
+      reinterpret_cast<void*>(stream));
+  check_rc(rc, "gtp_softmax_grad_bf16_cols");
+  return out;
+}
+
 TORCH_LIBRARY(graspo_tokpath, m) {
   m.def(
       "sample(Tensor logits, float temperature, int top_k, float top_p, float repetition_penalty, "
@@ -507,4 +567,9 @@ TORCH_LIBRARY(graspo_tokpath, m) {
   m.def("lm_head_logprob(Tensor hidden, Tensor weight, Tensor targets, int stream) -> "
         "(Tensor, Tensor, Tensor)",
         &lm_head_logprob);
+  m.def("lm_head_logprob_save(Tensor hidden, Tensor weight, Tensor targets, int stream) -> "
+        "(Tensor, Tensor, Tensor, Tensor)",
+        &lm_head_logprob_save);
+  m.def("softmax_grad_bf16(Tensor logits_t, Tensor grad_logprob, Tensor lse, int stream) -> Tensor",
+        &softmax_grad_bf16);
 }

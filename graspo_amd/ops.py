@@ -195,6 +195,28 @@ def lm_head_logprob(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.T
     return ops.lm_head_logprob(hidden, weight, targets, _stream(hidden))
 
 
+def lm_head_logprob_save(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor):
+    """(logprob, lse, logits_t, status) of ``hidden @ weight.T``: the fused
+    kernel of :func:`lm_head_logprob` that also writes the fp32 logits,
+    vocabulary-major (``logits_t`` [V, N] = the logits transposed), for the
+    backward, and the per-row status (a target outside [0, V) is
+    ``ROW_BAD_TARGET``)."""
+    ops = load()
+    targets = targets.reshape(-1).contiguous()
+    return ops.lm_head_logprob_save(hidden, weight, targets, _stream(hidden))
+
+
+def softmax_grad_bf16(logits_t: torch.Tensor, grad_logprob: torch.Tensor, lse: torch.Tensor):
+    """bf16 [V, N] of -g_n * softmax(logits[n]) for vocabulary-major fp32
+    ``logits_t`` [V, N] (unit column stride; ``lse`` each token's
+    log-sum-exp): the gradient of g * log_softmax(logits)[t] without its
+    one-hot term g * [v == t], transposed."""
+    ops = load()
+    return ops.softmax_grad_bf16(
+        logits_t, grad_logprob.reshape(-1).to(torch.float32).contiguous(),
+        lse.reshape(-1).to(torch.float32).contiguous(), _stream(logits_t))
+
+
 def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torch.Tensor,
                   eos_token_id: int, pad_token_id: int, sequences: torch.Tensor | None,
                   attention_mask: torch.Tensor | None, col: int, flags: torch.Tensor) -> None:

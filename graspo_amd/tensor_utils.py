@@ -119,25 +119,42 @@ def _broadcast_and_pad_finished(
 
 # ------------------------------------------------------------- logprobs
 
-def _matrix_core_operands(h2: torch.Tensor, weight: torch.Tensor):
+def _matrix_core_operands(h2: torch.Tensor, weight: torch.Tensor,
+                          targets: torch.Tensor | None = None):
     """bf16 operands for the chunk GEMMs, or None to multiply in the inputs'
     own dtype.
 
     bf16 / fp16 inputs are used as they are.  fp32 inputs -- the reference's
     callers pass ``hidden.float()`` and ``lm_head.weight.float()``, fp32
     copies of bf16 tensors -- are narrowed to bf16 in one pass that also
-    reports whether every value is a bf16 value (one host synchronisation).
-    When it is, a bf16 x bf16 product is exact in fp32, so a matrix-core GEMM
-    with fp32 output computes the same products as the reference's fp32 GEMM
-    (only the summation order differs); otherwise the fp32 GEMM is kept."""
+    reports whether every value is a bf16 value.  When it is, a bf16 x bf16
+    product is exact in fp32, so a matrix-core GEMM with fp32 output computes
+    the same products as the reference's fp32 GEMM (only the summation order
+    differs); otherwise the fp32 GEMM is kept.
+
+    With ``targets`` an id outside [0, V) raises, as the reference's
+    ``index_select`` does; that flag and the exactness flag are read in one
+    host synchronisation."""
+    V = weight.shape[0]
+    bad = None
+    if targets is not None and targets.numel():
+        bad = ((targets < 0) | (targets >= V)).any().to(torch.int32).view(1).to(h2.device)
+    mc, inexact = None, None
     if h2.dtype in (torch.bfloat16, torch.float16) and weight.dtype == h2.dtype:
-        return h2, weight
-    if h2.dtype == torch.float32 and weight.dtype == torch.float32 and h2.is_cuda:
+        mc = (h2, weight)
+    elif h2.dtype == torch.float32 and weight.dtype == torch.float32 and h2.is_cuda:
         hb, fh = ops.to_bf16_exact(h2)
         wb, fw = ops.to_bf16_exact(weight)
-        if int((fh | fw).item()) == 0:
-            return hb, wb
-    return None
+        mc, inexact = (hb, wb), fh | fw
+    flags = [f for f in (inexact, bad) if f is not None]
+    if flags:
+        vals = torch.cat(flags).tolist()
+        if bad is not None and vals[-1]:
+            raise RuntimeError(
+                "_selected_token_log_probs_from_hidden: an output id is outside [0, vocab_size)")
+        if inexact is not None and vals[0]:
+            mc = None
+    return mc
 
 
 def _chunk_logits(h2, weight, mc, start, chunk):
@@ -149,12 +166,16 @@ def _chunk_logits(h2, weight, mc, start, chunk):
 
 
 class _SelectedLogProbsFromHidden(torch.autograd.Function):
-    """log_softmax(h W^T)[target] without materialising [N, V] logits.  When
-    the operands are bf16 values (K a multiple of 128) the forward is one
-    fused kernel: the bf16 GEMM on the matrix cores with the log-sum-exp in
-    its epilogue.  Otherwise vocabulary chunks of the GEMM are folded into a
-    running (m, s) state by the lse kernel.  The backward recomputes each
-    chunk's softmax."""
+    """log_softmax(h W^T)[target] without materialising [N, V] logits for a
+    forward-only call.  When the operands are bf16 values (K a multiple of
+    128) the forward is one fused kernel: the bf16 GEMM on the matrix cores
+    with the log-sum-exp in its epilogue; when a gradient is wanted the same
+    kernel also keeps the fp32 logits, as the reference's autograd keeps
+    every chunk's logits for ``logsumexp``'s backward, and the backward is
+    one pass over them (bf16 of -g * softmax) and two bf16 GEMMs with fp32
+    output, the one-hot term g * [i == t] added in fp32.  Other operands
+    fold vocabulary chunks of the GEMM into a running (m, s) state with the
+    lse kernel and recompute each chunk's softmax in the backward."""
 
     @staticmethod
     def forward(ctx, hidden, weight, output_ids, chunk):
@@ -162,27 +183,32 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         h2 = hidden.reshape(-1, H)
         t = output_ids.reshape(-1)
         N, V = h2.shape[0], weight.shape[0]
-        # the reference's index_select / gather rejects an id outside [0, V)
-        if N and bool(((t < 0) | (t >= V)).any()):
-            raise RuntimeError(
-                "_selected_token_log_probs_from_hidden: an output id is outside [0, vocab_size)")
-        mc = _matrix_core_operands(h2, weight)
+        # raises for an id outside [0, V), as the reference's index_select does
+        mc = _matrix_core_operands(h2, weight, t)
+        logits = None
         if N and mc is not None and ops.lm_head_supported(*mc):
-            # one kernel: the bf16 GEMM with the log-sum-exp in its epilogue,
-            # no [N, V] logits (the vocabulary chunking is the kernel's tiling)
-            lp, _, lse = ops.lm_head_logprob(mc[0], mc[1], t)
+            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+                lp, lse, logits, _ = ops.lm_head_logprob_save(mc[0], mc[1], t)
+            else:
+                # one kernel: the bf16 GEMM with the log-sum-exp in its
+                # epilogue, no [N, V] logits (the vocabulary chunking is the
+                # kernel's tiling)
+                lp, _, lse = ops.lm_head_logprob(mc[0], mc[1], t)
         else:
             state = ops.new_lse_state(N, hidden.device)
             # (running each chunk's lse on a second stream beside the next
             # GEMM was slower: 21.4 against 16.5 ms at 8192 x 4096 x 248320)
             for c, start in enumerate(range(0, V, chunk)):
-                logits = _chunk_logits(h2, weight, mc, start, chunk)
-                ops.lse_partial(logits, t, start, state, accumulate=c > 0)
+                chunk_logits = _chunk_logits(h2, weight, mc, start, chunk)
+                ops.lse_partial(chunk_logits, t, start, state, accumulate=c > 0)
             lp, _ = ops.lse_finalize(state)
             lse = state[:, 0] + torch.log(state[:, 1])
         saved = (h2, weight, t, lse) + (mc if mc is not None else ())
+        if logits is not None:
+            saved = saved + (logits,)
         ctx.save_for_backward(*saved)
         ctx.has_mc = mc is not None
+        ctx.has_logits = logits is not None
         ctx.chunk = chunk
         ctx.out_shape = output_ids.shape
         return lp.view(output_ids.shape)
@@ -194,6 +220,25 @@ class _SelectedLogProbsFromHidden(torch.autograd.Function):
         mc = saved[4:6] if ctx.has_mc else None
         g = grad_out.reshape(-1).to(torch.float32)
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if ctx.has_logits:
+            # d lp_n / d x_ni = [i == t_n] - p_ni: the softmax part in bf16
+            # (each element within 2^-8 of -g p) through the matrix cores,
+            # the one-hot part in fp32
+            # (vocabulary-major: gs_t is [V, N])
+            hb, wb = mc
+            gs_t = ops.softmax_grad_bf16(saved[6], g, lse)
+            tl = t.long()
+            gt = g.unsqueeze(1)
+            grad_h = grad_w = None
+            if need_h:
+                grad_h = torch.mm(gs_t.t(), wb, out_dtype=torch.float32)
+                grad_h += gt * wb.index_select(0, tl).float()
+                grad_h = grad_h.to(h2.dtype).view(*ctx.out_shape, h2.shape[-1])
+            if need_w:
+                grad_w = torch.mm(gs_t, hb, out_dtype=torch.float32)
+                grad_w.index_add_(0, tl, gt * hb.float())
+                grad_w = grad_w.to(weight.dtype)
+            return grad_h, grad_w, None, None
         # the bf16 route accumulates grad_h over the chunks in fp32
         acc_dtype = torch.float32 if mc is not None else h2.dtype
         grad_h = torch.zeros(h2.shape, dtype=acc_dtype, device=h2.device) if need_h else None
@@ -245,9 +290,13 @@ def _selected_token_log_probs_from_hidden(
     the reference's ``vocab_chunk_size`` GEMMs with the lse kernel as the
     logsumexp / logaddexp fold.
     Differentiable in ``hidden_states`` and ``lm_head_weight``; on the bf16
-    route the gradient GEMMs also run on matrix cores, with the fp32 softmax
-    gradient split into two bf16 parts (hi + lo, within 2^-16 of it), so the
-    gradients carry about 16 significant bits."""
+    route the gradient GEMMs also run on matrix cores.  With the fused
+    forward (K a multiple of 128) the softmax part of the logit gradient,
+    -g * p, is rounded once to bf16 (each element within 2^-8 of it) and the
+    one-hot part g * [i == t] is added in fp32, so a gradient element is
+    within 2^-8 * sum_i |g p_i w_i| of the fp32 one; the chunked route
+    splits the fp32 logit gradient into two bf16 parts (hi + lo, within
+    2^-16 of it)."""
     return _SelectedLogProbsFromHidden.apply(
         hidden_states, lm_head_weight, output_ids, int(vocab_chunk_size)
     )

@@ -261,6 +261,25 @@ int gtp_lm_head_logprob_rows(const uint16_t* hidden, int64_t N, int64_t K,
 size_t gtp_lm_head_workspace_bytes(int64_t N, int64_t V);
 
 /*
+ * gtp_lm_head_logprob_save_rows -- gtp_lm_head_logprob_rows that also writes
+ * the fp32 logits x = h W^T, vocabulary-major: out_logits[v * logits_stride
+ * + n] = x[n, v], for a backward pass.  Under autograd the reference keeps
+ * the same bytes: torch.logsumexp saves each chunk's fp32 logits for its
+ * backward (tensor_utils.py:180-184, called with grad enabled at
+ * models/qwen35_36/training.py:407-427).
+ * Arguments as gtp_lm_head_logprob_rows, plus
+ *   out_logits    [V, logits_stride] fp32, 4-byte aligned, logits_stride >= N
+ *                 (the first N of each vocabulary row are written).
+ */
+int gtp_lm_head_logprob_save_rows(const uint16_t* hidden, int64_t N, int64_t K,
+                                  int64_t hidden_stride, const uint16_t* weight, int64_t V,
+                                  int64_t weight_stride, const void* targets,
+                                  int targets_int64, float* out_logprob, float* out_entropy,
+                                  float* out_lse, int32_t* out_status, float* out_logits,
+                                  int64_t logits_stride, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/*
  * gtp_logprob_backward_rows -- gradient of log_softmax(x)[target] with respect
  * to the logits, scaled by the incoming gradient of each row:
  *   grad[i] = g * ([i == target - col_offset] - exp(x_i - lse))
@@ -288,6 +307,23 @@ int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N,
                               int targets_int64, const float* grad_logprob,
                               const float* lse, void* grad,
                               int64_t grad_stride, void* stream);
+
+/*
+ * gtp_softmax_grad_bf16_cols -- grad_t[v, n] = bf16(-g_n exp(x_t[v, n] - lse_n))
+ * of vocabulary-major fp32 logits (the layout gtp_lm_head_logprob_save_rows
+ * writes), rounded to nearest even: the softmax part of the gradient of
+ * g_n log_softmax(x_n)[t_n] without its one-hot term g_n [v == t_n], which
+ * the caller adds in fp32.  Each element is within 2^-8 of -g p.  Feeds the
+ * hidden-state path's backward (tensor_utils.py:167-186 under autograd):
+ * bf16 matrix-core GEMMs of it against the exact bf16 operands, fp32 output.
+ *   logits_t  [V, logits_stride] fp32 (the first N of each row are read)
+ *   grad_logprob, lse  [N] fp32; a token with g == 0 gets zeros
+ *   grad_t    [V, grad_stride] bf16
+ */
+int gtp_softmax_grad_bf16_cols(const float* logits_t, int64_t V, int64_t N,
+                               int64_t logits_stride, const float* grad_logprob,
+                               const float* lse, uint16_t* grad_t, int64_t grad_stride,
+                               void* stream);
 
 /*
  * gtp_logprob_backward_split_rows -- the gradient of gtp_logprob_backward_rows

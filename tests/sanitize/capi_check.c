@@ -190,6 +190,34 @@ int main(void) {
   EXPECT_RC(w, gtp_lm_head_logprob_rows(NULL, 0, 128, 128, NULL, 1000, 128, NULL, 0, NULL, NULL,
                                         NULL, NULL, NULL, 0, NULL), OK);
 
+  float* LG = PH(float*);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                             NULL, NULL, NULL, 256, wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                             NULL, NULL, LG, 255, wsp, wsz, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                             NULL, NULL, (float*)(uintptr_t)0x1002, 256, wsp,
+                                             wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                             NULL, NULL, LG, (int64_t)1 << 40, wsp, wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 192, 192, WB, 1000, 192, T, 0, o, NULL,
+                                             NULL, NULL, LG, 256, wsp, wsz, NULL), X);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(HB, 256, 128, 128, WB, 1000, 128, T, 0, o, NULL,
+                                             NULL, NULL, LG, 256, wsp, wsz - 1, NULL), I);
+  EXPECT_RC(w, gtp_lm_head_logprob_save_rows(NULL, 0, 128, 128, NULL, 1000, 128, NULL, 0, NULL,
+                                             NULL, NULL, NULL, NULL, 0, NULL, 0, NULL), OK);
+
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, -1, 10, F, F, h, 10, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 3, F, F, h, 10, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, h, 3, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 0, 4, 4, F, F, h, 4, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, NULL, F, h, 4, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, NULL, 4, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, INT64_MAX, INT64_MAX, F, F, h, INT64_MAX, NULL),
+            X);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, INT64_MAX, 4, 4, F, F, h, 4, NULL), X);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(NULL, 10, 0, 0, NULL, NULL, NULL, 0, NULL), OK);
+
   EXPECT_RC(w, strstr(gtp_version(), "gfx950") != NULL, 1);
 
   printf("C-ABI sanitizer checks: %d run, %d failed\n", g_checks, g_fails);

@@ -165,3 +165,45 @@ def test_fp32_top_p_rows_take_the_bf16_kernel_when_exact(exact):
     if exact:
         idsb = TU._next_token_from_logits(xb.to(DEV), **kw)
         assert torch.equal(ids32, idsb)
+
+
+def test_hidden_path_gradients_on_the_fused_route(monkeypatch):
+    """K a multiple of 128: the forward keeps the fused kernel's fp32 logits
+    and the backward runs bf16(-g p) through two matrix-core GEMMs, adding
+    the one-hot term g [i == t] in fp32.  Each gradient element is within
+    2^-8 * sum_i |g p_i w_i| (the bf16 rounding of -g p; doubled here for
+    the fp32 sums) of the fp64 gradient; a missing or misplaced one-hot term
+    is off by |g w_t| ~ the whole sum."""
+    calls = []
+    real = ops.lm_head_logprob_save
+    monkeypatch.setattr(ops, "lm_head_logprob_save", lambda *a: calls.append(1) or real(*a))
+    g = torch.Generator().manual_seed(9)
+    B, S, H, V = 2, 150, 256, 5077
+    h = torch.randn(B, S, H, generator=g).to(torch.bfloat16).float().to(DEV).requires_grad_(True)
+    w = (torch.randn(V, H, generator=g) * 0.1).to(torch.bfloat16).float().to(DEV)
+    w.requires_grad_(True)
+    ids = torch.randint(0, V, (B, S), generator=g).to(DEV)
+    ids[0, :4] = ids[1, 7]  # a target shared by several tokens (index_add of the one-hot term)
+    gout = torch.randn(B, S, generator=g).to(DEV)
+    gout[1, 3] = 0.0
+    print("fused-route gradients", flush=True)
+    out = TU._selected_token_log_probs_from_hidden(h, w, ids)
+    (out * gout).sum().backward()
+    assert calls, "the fused route with saved logits was not taken"
+    h2 = h.detach().double().requires_grad_(True)
+    w2 = w.detach().double().requires_grad_(True)
+    logits = h2 @ w2.t()
+    ref = logits.gather(-1, ids.unsqueeze(-1)).squeeze(-1) - torch.logsumexp(logits, -1)
+    (ref * gout.double()).sum().backward()
+    assert float((out.double() - ref).abs().max()) <= 1e-4
+    p = torch.softmax(logits.detach(), -1).view(-1, V)
+    gp = (gout.double().view(-1, 1).abs() * p)                       # |g| p  [N, V]
+    bound_h = 2.0 ** -7 * (gp @ w2.detach().abs()) + 1e-6            # [N, H]
+    bound_w = 2.0 ** -7 * (gp.t() @ h2.detach().abs().view(-1, H)) + 1e-6  # [V, H]
+    err_h = (h.grad.double().view(-1, H) - h2.grad.view(-1, H)).abs()
+    err_w = (w.grad.double() - w2.grad).abs()
+    assert bool((err_h <= bound_h).all()), float((err_h - bound_h).max())
+    assert bool((err_w <= bound_w).all()), float((err_w - bound_w).max())
+    # the one-hot term alone is far outside the bound
+    onehot = gout.double().view(-1, 1).abs() * w2.detach()[ids.view(-1)].abs()
+    assert float((onehot - bound_h).max()) > 0

@@ -107,3 +107,67 @@ def test_full_size_sampled_rows():
     clp, cent = ops.lse_finalize(state)
     assert (lp - clp).abs().max().item() <= 2 * TOL
     assert (ent - cent).abs().max().item() <= 2 * TOL
+
+
+def test_strided_weight_rows():
+    """lm_head weight rows farther apart than K (a column slice of a wider
+    matrix): the buffer ranges and offsets follow the row stride."""
+    g = torch.Generator(device="cuda:0").manual_seed(9)
+    K = 512
+    big = (torch.randn(3000, K + 136, generator=g, device="cuda:0") / K ** 0.5).to(torch.bfloat16)
+    w = big[:, 64:64 + K]  # rows 648 elements apart, 128-byte offset
+    h, _, t = _case(300, 3000, K, seed=10)
+    assert w.stride(0) == K + 136
+    _check(h, w, t, "strided weight")
+
+
+@pytest.mark.parametrize("N,V,K", [(300, 1037, 256), (257, 300, 128), (1, 256, 128),
+                                   (512, 100, 384), (1000, 40001, 1024)])
+def test_save_keeps_the_logits(N, V, K):
+    """gtp_lm_head_logprob_save_rows: the same logprob and lse as the kernel
+    that writes no logits, and every logit of the product, vocabulary-major
+    (token and vocabulary tails, a vocabulary below one tile), within 1e-4
+    of fp64; a bad target is NaN with its status."""
+    h, w, t = _case(N, V, K, seed=N + 2 * V + K)
+    if N > 3:
+        t[3] = V
+    print("lm_head save:", (N, V, K), flush=True)
+    lp, lse, logits_t, status = ops.lm_head_logprob_save(h, w, t)
+    lp0, _, lse0 = ops.lm_head_logprob(h, w, t)
+    torch.cuda.synchronize()
+    assert tuple(logits_t.shape) == (V, N) and logits_t.dtype == torch.float32
+    x = h.double() @ w.double().t()
+    assert (logits_t.t().double() - x).abs().max().item() <= TOL
+    ok = torch.ones(N, dtype=torch.bool, device=lp.device)
+    if N > 3:
+        ok[3] = False
+        assert torch.isnan(lp[3]) and int(status[3]) == ops.ROW_BAD_TARGET
+    assert bool((status[ok] == ops.ROW_OK).all())
+    assert (lp[ok] - lp0[ok]).abs().max().item() <= 1e-6
+    assert (lse - lse0).abs().max().item() <= 1e-6
+    rlp, _, rlse = fp64_reference(h, w, t)
+    assert (lp[ok].double() - rlp[ok]).abs().max().item() <= TOL
+    assert (lse.double() - rlse).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("N,V,stride", [(4099, 300, 4099), (8192, 2000, 8192), (1000, 77, 1004),
+                                        (3, 5000, 3)])
+def test_softmax_grad_bf16(N, V, stride):
+    """bf16(-g_n softmax(x_n)) of vocabulary-major logits: within 2^-8 of the
+    fp64 value (plus the fp32 evaluation's ~3e-6 relative), zeros for a
+    token with g == 0, any row stride and token tail."""
+    g0 = torch.Generator(device="cuda:0").manual_seed(N + V)
+    big = torch.randn(V, stride, generator=g0, device="cuda:0") * 3.0
+    xt = big[:, :N]                     # [V, N], token n's logits are column n
+    xt[9, min(4, N - 1)] = 50.0         # p ~ 1 at one token
+    g = torch.randn(N, generator=g0, device="cuda:0")
+    g[min(2, N - 1)] = 0.0
+    lse = torch.logsumexp(xt.double(), dim=0).float()
+    print("softmax grad:", N, V, stride, flush=True)
+    gs = ops.softmax_grad_bf16(xt, g, lse)
+    torch.cuda.synchronize()
+    assert gs.dtype == torch.bfloat16 and tuple(gs.shape) == (V, N)
+    ref = -g.double().unsqueeze(0) * torch.exp(xt.double() - lse.double().unsqueeze(0))
+    err = (gs.double() - ref).abs() - (2.0 ** -8 + 1e-5) * ref.abs() - 1e-38
+    assert err.max().item() <= 0.0
+    assert not bool(gs[:, min(2, N - 1)].float().any())
