@@ -2164,13 +2164,13 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
       unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
       const dim3 sgrid((unsigned)sp.S, (unsigned)B);
       switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-        case 0: launch_timed(sampler_topps_kernel<0>, sgrid, block, s, a, ws, sp.vps); break;
-        case 1: launch_timed(sampler_topps_kernel<1>, sgrid, block, s, a, ws, sp.vps); break;
-        case 2: launch_timed(sampler_topps_kernel<2>, sgrid, block, s, a, ws, sp.vps); break;
-        default: launch_timed(sampler_topps_kernel<3>, sgrid, block, s, a, ws, sp.vps); break;
+        case 0: launch_timed_head(sampler_topps_kernel<0>, sgrid, block, s, a, ws, sp.vps); break;
+        case 1: launch_timed_head(sampler_topps_kernel<1>, sgrid, block, s, a, ws, sp.vps); break;
+        case 2: launch_timed_head(sampler_topps_kernel<2>, sgrid, block, s, a, ws, sp.vps); break;
+        default: launch_timed_head(sampler_topps_kernel<3>, sgrid, block, s, a, ws, sp.vps); break;
       }
-      hipLaunchKernelGGL(sampler_handover_kernel<uint16_t>, grid, block, 0, s, a,
-                         reinterpret_cast<uint32_t*>(workspace));
+      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a,
+                        reinterpret_cast<uint32_t*>(workspace));
       return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
     }
   }
@@ -2178,24 +2178,24 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
     // fp32 top-p rows: two reads, the candidates of the cut in LDS
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
     switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-      case 0: launch_timed(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
-      case 1: launch_timed(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
-      case 2: launch_timed(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
-      default: launch_timed(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
+      case 0: launch_timed_head(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
+      case 1: launch_timed_head(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
+      case 2: launch_timed_head(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
+      default: launch_timed_head(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
     }
-    hipLaunchKernelGGL(sampler_handover_kernel<float>, grid, block, 0, s, a, handover);
+    launch_timed_tail(sampler_handover_kernel<float>, grid, block, s, a, handover);
     return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
   }
   if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
       workspace_bytes >= tw) {
     uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
     switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-      case 0: launch_timed(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
-      case 1: launch_timed(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
-      case 2: launch_timed(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
-      default: launch_timed(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
+      case 0: launch_timed_head(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
+      case 1: launch_timed_head(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
+      case 2: launch_timed_head(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
+      default: launch_timed_head(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
     }
-    hipLaunchKernelGGL(sampler_handover_kernel<uint16_t>, grid, block, 0, s, a, handover);
+    launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
     return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
   }
   if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&

@@ -424,12 +424,13 @@ int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
 /*
  * gtp_time_next_launch -- measurement hook, no counterpart in the reference:
  * the next gtp_sample_rows, gtp_logprob_entropy_rows, gtp_logprob_backward_rows
- * or gtp_stream_read_rows kernel launched from the calling thread records
- * start_event when its dispatch begins and
- * stop_event when it ends (hipExtLaunchKernelGGL), so the two HIP events
- * bracket the kernel alone, without the idle time of event packets recorded
- * around it.  Both are hipEvent_t created by the caller (with timing).  The
- * hook is per thread and used once; the benchmark is its caller.
+ * or gtp_stream_read_rows call from the calling thread records start_event
+ * when its first kernel's dispatch begins and stop_event when its last
+ * kernel ends (hipExtLaunchKernelGGL; a top-p sampler call launches its
+ * kernel and the hand-over kernel), so the two HIP events bracket the call's
+ * kernels, without the idle time of event packets recorded around them.
+ * Both are hipEvent_t created by the caller (with timing).  The hook is per
+ * thread and used once; the benchmark is its caller.
  */
 int gtp_time_next_launch(void* start_event, void* stop_event);
 

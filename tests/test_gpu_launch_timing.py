@@ -64,3 +64,31 @@ def test_hook_needs_existing_events():
     with pytest.raises(RuntimeError):
         ops.time_next_launch(torch.cuda.Event(enable_timing=True),
                              torch.cuda.Event(enable_timing=True))
+
+
+def test_hook_brackets_both_launches_of_a_top_p_call():
+    """A top-p call launches its kernel and the hand-over kernel: the events
+    span both, so a row handed over to the row-wise path (a -inf logit is
+    outside the top-p kernel's bins) adds its time to the hooked interval."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = (torch.randn(128, 151936, device=DEV, generator=g) * 2.0).to(torch.bfloat16)
+    u = ops.draw_uniforms(128, DEV, g)
+    kw = dict(temperature=0.7, top_p=0.9, uniforms=u)
+    xh = x.clone()
+    xh[5, 77] = float("-inf")
+    times = {}
+    for name, xx in (("plain", x), ("handed_over", xh)):
+        ops.sample(xx, **kw)  # warm
+        k0, k1 = _events()
+        o0, o1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ops.time_next_launch(k0, k1)
+        o0.record()
+        out = ops.sample(xx, **kw)
+        o1.record()
+        torch.cuda.synchronize()
+        times[name] = (k0.elapsed_time(k1), o0.elapsed_time(o1))
+        assert bool((out.status == 0).all())
+    print("top-p call (hooked, around):", times, flush=True)
+    (t0, a0), (t1, a1) = times["plain"], times["handed_over"]
+    assert 0.0 < t0 <= a0 and 0.0 < t1 <= a1
+    assert t1 - t0 > 0.5 * (a1 - a0) > 0.0
