@@ -2135,89 +2135,113 @@ size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_p
   return sp.S ? sp.bytes : topp_list_bytes(B);
 }
 
+GeneralRoute route_general(int dtype, int64_t B, int64_t V, bool aligned, int64_t hist_len,
+                           bool has_mask, const gtp_sampler_params* p, bool has_ws,
+                           size_t workspace_bytes) {
+  GeneralRoute r{GTP_ROUTE_ROWWISE, ToppSplit{0, 0, 0}};
+  // top-p rows without top-k: the single-read top-p kernels, then the
+  // row-wise path for any row they hand over (the hand-over list lives in the
+  // workspace; without one, the value-histogram kernel takes the call)
+  const size_t tw = topp_takes(dtype, B, V, p) ? topp_list_bytes(B) : 0;
+  const bool pen = hist_len > 0 && p->repetition_penalty != 1.0f;
+  // (penalised counts are 16-bit: at most 65535 history entries)
+  // (rows with a mask and no penalty: the split kernel gains nothing from
+  // 32 rows on, [64, 151936] 43.4 against 42.1 us)
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535 && has_ws &&
+      (pen || !has_mask || B <= 32)) {
+    // few bf16 rows: each row split over S workgroups (the workspace holds
+    // their counters, headers and slots)
+    const ToppSplit sp = plan_topp_split(dtype, B, V, p, workspace_bytes);
+    if (sp.S >= 2) {
+      r.route = GTP_ROUTE_TOPP_SPLIT;
+      r.split = sp;
+      return r;
+    }
+  }
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_F32 && has_ws && workspace_bytes >= tw) {
+    r.route = GTP_ROUTE_TOPP32;  // two reads, the candidates of the cut in LDS
+    return r;
+  }
+  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535 && has_ws &&
+      workspace_bytes >= tw) {
+    r.route = GTP_ROUTE_TOPP;
+    return r;
+  }
+  // bf16 sampling rows on 16-byte aligned rows: the value-histogram kernel
+  // (temperature bounded so that distinct bf16 values keep distinct, normal
+  // y = x / T)
+  if (dtype == GTP_DTYPE_BF16 && aligned && p->temperature > 0.0f && p->temperature <= 1024.0f &&
+      hist_len <= 65535)
+    r.route = GTP_ROUTE_HIST;
+  return r;
+}
+
 // One workgroup of 1024 threads per row; handles every row layout, vocabulary
 // and parameter combination the contract allows.
 int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
                            void* workspace, size_t workspace_bytes) {
   const dim3 grid((unsigned)B), block(kSB);
-  // bf16 sampling rows on 16-byte aligned rows take the value-histogram
-  // kernel (temperature bounded so that distinct bf16 values keep distinct,
-  // normal y = x / T)
   const int64_t es = dtype == GTP_DTYPE_F32 ? 4 : 2;
   const bool aligned = (reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0 &&
                        ((a.row_stride * es) & 15) == 0;
-  // (penalised counts are 16-bit: at most 65535 history entries)
-  // top-p rows without top-k: the single-read top-p kernel, then the
-  // row-wise path for any row it hands over (the hand-over list lives in the
-  // workspace; without one, the value-histogram kernel below takes the call)
   gtp_sampler_params p{a.T, a.K, a.P, a.rho};
-  const size_t tw = topp_takes(dtype, B, a.V, &p) ? topp_list_bytes(B) : 0;
   const bool pen = a.hist && a.hist_len > 0 && a.rho != 1.0f;
-  // (rows with a mask and no penalty: the split kernel gains nothing from
-  // 32 rows on, [64, 151936] 43.4 against 42.1 us)
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
-      (pen || !a.mask || B <= 32)) {
-    // few bf16 rows: each row split over S workgroups (the workspace holds
-    // their counters, headers and slots)
-    const ToppSplit sp = plan_topp_split(dtype, B, a.V, &p, workspace_bytes);
-    if (sp.S >= 2) {
+  const int mode = (a.mask ? 2 : 0) | (pen ? 1 : 0);
+  const GeneralRoute r = route_general(dtype, B, a.V, aligned, a.hist ? a.hist_len : 0,
+                                       a.mask != nullptr, &p, workspace != nullptr,
+                                       workspace_bytes);
+  uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
+  switch (r.route) {
+    case GTP_ROUTE_TOPP_SPLIT: {
       unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
-      const dim3 sgrid((unsigned)sp.S, (unsigned)B);
-      switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-        case 0: launch_timed_head(sampler_topps_kernel<0>, sgrid, block, s, a, ws, sp.vps); break;
-        case 1: launch_timed_head(sampler_topps_kernel<1>, sgrid, block, s, a, ws, sp.vps); break;
-        case 2: launch_timed_head(sampler_topps_kernel<2>, sgrid, block, s, a, ws, sp.vps); break;
-        default: launch_timed_head(sampler_topps_kernel<3>, sgrid, block, s, a, ws, sp.vps); break;
+      const dim3 sgrid((unsigned)r.split.S, (unsigned)B);
+      switch (mode) {
+        case 0: launch_timed_head(sampler_topps_kernel<0>, sgrid, block, s, a, ws, r.split.vps); break;
+        case 1: launch_timed_head(sampler_topps_kernel<1>, sgrid, block, s, a, ws, r.split.vps); break;
+        case 2: launch_timed_head(sampler_topps_kernel<2>, sgrid, block, s, a, ws, r.split.vps); break;
+        default: launch_timed_head(sampler_topps_kernel<3>, sgrid, block, s, a, ws, r.split.vps); break;
       }
-      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a,
-                        reinterpret_cast<uint32_t*>(workspace));
-      return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
-    }
-  }
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_F32 && workspace && workspace_bytes >= tw) {
-    // fp32 top-p rows: two reads, the candidates of the cut in LDS
-    uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
-    switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-      case 0: launch_timed_head(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
-      case 1: launch_timed_head(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
-      case 2: launch_timed_head(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
-      default: launch_timed_head(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
-    }
-    launch_timed_tail(sampler_handover_kernel<float>, grid, block, s, a, handover);
-    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
-  }
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && a.hist_len <= 65535 && workspace &&
-      workspace_bytes >= tw) {
-    uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
-    switch ((a.mask ? 2 : 0) | (pen ? 1 : 0)) {
-      case 0: launch_timed_head(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
-      case 1: launch_timed_head(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
-      case 2: launch_timed_head(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
-      default: launch_timed_head(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
-    }
-    launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
-    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
-  }
-  if (dtype == GTP_DTYPE_BF16 && aligned && a.T > 0.0f && a.T <= 1024.0f &&
-      a.hist_len <= 65535) {
-    if (a.mask)
-      launch_timed(sampler_hist_kernel<uint16_t, true>, grid, block, s, a);
-    else
-      launch_timed(sampler_hist_kernel<uint16_t, false>, grid, block, s, a);
-    return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
-  }
-  switch (dtype) {
-    case GTP_DTYPE_BF16:
-      launch_timed(sampler_rowwise_kernel<uint16_t>, grid, block, s, a);
+      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
       break;
-    case GTP_DTYPE_F16:
-      launch_timed(sampler_rowwise_kernel<_Float16>, grid, block, s, a);
+    }
+    case GTP_ROUTE_TOPP32:
+      switch (mode) {
+        case 0: launch_timed_head(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
+        case 1: launch_timed_head(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
+        case 2: launch_timed_head(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
+        default: launch_timed_head(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
+      }
+      launch_timed_tail(sampler_handover_kernel<float>, grid, block, s, a, handover);
       break;
-    case GTP_DTYPE_F32:
-      launch_timed(sampler_rowwise_kernel<float>, grid, block, s, a);
+    case GTP_ROUTE_TOPP:
+      switch (mode) {
+        case 0: launch_timed_head(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
+        case 1: launch_timed_head(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
+        case 2: launch_timed_head(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
+        default: launch_timed_head(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
+      }
+      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
+      break;
+    case GTP_ROUTE_HIST:
+      if (a.mask)
+        launch_timed(sampler_hist_kernel<uint16_t, true>, grid, block, s, a);
+      else
+        launch_timed(sampler_hist_kernel<uint16_t, false>, grid, block, s, a);
       break;
     default:
-      return GTP_ERR_INVALID_ARGUMENT;
+      switch (dtype) {
+        case GTP_DTYPE_BF16:
+          launch_timed(sampler_rowwise_kernel<uint16_t>, grid, block, s, a);
+          break;
+        case GTP_DTYPE_F16:
+          launch_timed(sampler_rowwise_kernel<_Float16>, grid, block, s, a);
+          break;
+        case GTP_DTYPE_F32:
+          launch_timed(sampler_rowwise_kernel<float>, grid, block, s, a);
+          break;
+        default:
+          return GTP_ERR_INVALID_ARGUMENT;
+      }
   }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }

@@ -1403,6 +1403,26 @@ extern "C" size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
   return pl.fast ? pl.ws_bytes : topp_workspace_bytes(dtype, B, V, params, SIZE_MAX);
 }
 
+extern "C" int gtp_sample_route(int dtype, int64_t B, int64_t V, int aligned, int64_t hist_len,
+                                int has_mask, const gtp_sampler_params* params,
+                                size_t workspace_bytes, int32_t* out_route, int32_t* out_slices) {
+  if (!params || !out_route || B <= 0 || V <= 0 || hist_len < 0) return GTP_ERR_INVALID_ARGUMENT;
+  if (dtype != GTP_DTYPE_F32 && dtype != GTP_DTYPE_BF16 && dtype != GTP_DTYPE_F16)
+    return GTP_ERR_INVALID_ARGUMENT;
+  if (V > GTP_SAMPLER_MAX_V || B > 0x7FFFFFFFll) return GTP_ERR_UNSUPPORTED;
+  const FastPlan pl = plan_fast(dtype, B, V, params, aligned != 0);
+  if (pl.fast) {
+    *out_route = GTP_ROUTE_SPLIT_TOPK;
+    if (out_slices) *out_slices = pl.S;
+    return GTP_OK;
+  }
+  const GeneralRoute r = route_general(dtype, B, V, aligned != 0, hist_len, has_mask != 0, params,
+                                       workspace_bytes > 0, workspace_bytes);
+  *out_route = r.route;
+  if (out_slices) *out_slices = r.route == GTP_ROUTE_TOPP_SPLIT ? r.split.S : 1;
+  return GTP_OK;
+}
+
 namespace gtp {
 
 // gtp_sample_rows with its workspace; `clear_counters` zeroes the per-row

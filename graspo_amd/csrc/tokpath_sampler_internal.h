@@ -38,6 +38,7 @@ struct SamplerArgs {
 int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
                            void* workspace, size_t workspace_bytes);
 
+
 // The first kWsZeroBytes of a sampler workspace are words that every call
 // leaves zero: the top-p kernels' hand-over count, arrival counter and list
 // (words 0, 1, 2..), the split kernel's per-row arrival counters (words
@@ -62,6 +63,19 @@ struct ToppSplit {
   size_t bytes;
 };
 ToppSplit plan_topp_split(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap);
+
+// Which kernel launch_sampler_general runs for a call (GTP_ROUTE_*, never
+// GTP_ROUTE_SPLIT_TOPK), and the split top-p kernel's plan when it takes the
+// call.  The one decision both the launch and gtp_sample_route use.
+struct GeneralRoute {
+  int route;
+  ToppSplit split;
+};
+// aligned: 16-byte aligned logits and row stride; hist_len: history entries
+// per row (0 without a history); has_ws: a workspace was passed.
+GeneralRoute route_general(int dtype, int64_t B, int64_t V, bool aligned, int64_t hist_len,
+                           bool has_mask, const gtp_sampler_params* p, bool has_ws,
+                           size_t workspace_bytes);
 
 // Workspace of the top-p path for these parameters within `cap` bytes (0
 // when another path takes the call): the split kernel's counters, headers

@@ -29,6 +29,12 @@
 // one-workgroup kernel.
 #pragma once
 
+// The publication of slice counts below relies on gfx950's code generation
+// (see the arrival step of topps_row).
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "tokpath_sampler_topps.h: the split top-p publication protocol is written for gfx950"
+#endif
+
 namespace gtp {
 namespace topps {
 
@@ -352,6 +358,16 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
   // increment of the row's counter announces the slice; the last workgroup
   // to arrive has seen every increment, and its acquire fence (an L1 and L2
   // invalidate) makes the other slots visible to its waves.
+  //
+  // This publication has no release operation, so the HIP/LLVM memory model
+  // alone gives it no happens-before edge: it rests on gfx950's code
+  // generation, where agent-scope stores write through to L2 and vmcnt(0)
+  // waits for their completion, and on nothing being moved past the
+  // barrier.  A release fence here would add an L2 write-back (buffer_wbl2)
+  // per workgroup, 8-10 us per arrival with 32 workgroups per XCD.  The file
+  // refuses to build for any other target (below), and the reader's loads
+  // are relaxed agent-scope atomics of the same 64-bit words the writers
+  // store.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
   __syncthreads();
   if (tid == 0) {
@@ -371,7 +387,8 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
   // ---- 5. merge the other slices' counts into the bins
   const uint32_t* hrow = split_headers(ws) + (size_t)b * S * kHdrWords;
   const uint32_t* srow = split_slots(ws, B, S) + (size_t)b * S * kSlotWords;
-  if (tid < S * kHdrWords) (&ex.hd[0][0])[tid] = hrow[tid];
+  if (tid < S * kHdrWords)
+    (&ex.hd[0][0])[tid] = __hip_atomic_load(hrow + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   {
     uint32_t uA = 0xFFFFFFFFu, vA = 0u, u2 = 0xFFFFFFFFu, v2 = 0u;  // the union of the ranges
@@ -396,7 +413,12 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
 #pragma unroll
         for (int j = 0; j < kMaxS; ++j) {
           if (j < S && j != s && 4u * q >= ex.hd[j][rw] && 4u * q < ex.hd[j][rw + 1]) {
-            const u32x4 v = reinterpret_cast<const u32x4*>(srow + (size_t)j * kSlotWords)[q];
+            // the two 64-bit words the slice's writer stored
+            const unsigned long long* d =
+                reinterpret_cast<const unsigned long long*>(srow + (size_t)j * kSlotWords) + 2 * q;
+            const unsigned long long w0 = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned long long w1 = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const u32x4 v = {(uint32_t)w0, (uint32_t)(w0 >> 32), (uint32_t)w1, (uint32_t)(w1 >> 32)};
             lo4 += v & 0xFFFFu;
             hi4 += v >> 16;
           }
@@ -563,7 +585,10 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
       if (v < 0) return 0u;
       const uint32_t w = region + vb_word(v);
       if (w < ex.hd[j][rw] || w >= ex.hd[j][rw + 1]) return 0u;
-      return (srow[(size_t)j * kSlotWords + w] >> vb_shift(v)) & 0xFFFFu;
+      const unsigned long long d = __hip_atomic_load(
+          reinterpret_cast<const unsigned long long*>(srow + (size_t)j * kSlotWords) + (w >> 1),
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return ((uint32_t)(d >> (32 * (w & 1))) >> vb_shift(v)) & 0xFFFFu;
     };
     uint32_t c0 = 0u, c1 = 0u;
     if (ok && lane < S) {

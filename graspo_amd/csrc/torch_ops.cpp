@@ -1,6 +1,6 @@
 // torch_ops.cpp -- thin PyTorch-ROCm binding of the C ABI (host-only C++).
 //
-// Registers torch.ops.graspo_tokpath.{sample, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
+// Registers torch.ops.graspo_tokpath.{sample, sample_route, logprob_entropy, logprob_backward, graspo_loss_*, lse_partial,
 // lse_finalize, decode_update, to_bf16_exact, logprob_backward_split, time_next_launch,
 // lm_head_logprob, lm_head_logprob_save, softmax_grad_bf16}.  Each op validates its tensors (TORCH_CHECK surfaces as a
 // Python RuntimeError), allocates the outputs on the logits' device, and
@@ -153,6 +153,33 @@ SampleOut sample(const at::Tensor& logits, double temperature, int64_t top_k, do
       reinterpret_cast<void*>(stream));
   check_rc(rc, "gtp_sample_rows");
   return {ids, lp, slp, kept, tv, tid, st};
+}
+
+// The kernel `sample` would run for these logits and parameters (with the
+// workspace it would pass): (GTP_ROUTE_*, workgroups per row).
+std::tuple<int64_t, int64_t> sample_route(const at::Tensor& logits, double temperature,
+                                          int64_t top_k, double top_p, double repetition_penalty,
+                                          int64_t hist_len, bool has_mask) {
+  check_rows(logits, "logits");
+  const int64_t B = logits.size(0), V = logits.size(1);
+  TORCH_CHECK(B > 0 && V > 0 && V <= GTP_SAMPLER_MAX_V && top_k >= 0 && top_k <= INT32_MAX &&
+                  hist_len >= 0,
+              "graspo_tokpath.sample_route: bad shape or parameters");
+  gtp_sampler_params p;
+  p.temperature = (float)temperature;
+  p.top_k = (int32_t)top_k;
+  p.top_p = (float)top_p;
+  p.repetition_penalty = (float)repetition_penalty;
+  const int dt = dtype_code(logits);
+  const size_t ws_bytes = gtp_sample_workspace_bytes(dt, B, V, &p);
+  const int64_t es = logits.element_size();
+  const bool aligned = (reinterpret_cast<uintptr_t>(logits.data_ptr()) & 15u) == 0 &&
+                       ((uint64_t)(row_stride_of(logits) * es) & 15u) == 0;
+  int32_t route = 0, slices = 0;
+  check_rc(gtp_sample_route(dt, B, V, aligned ? 1 : 0, hist_len, has_mask ? 1 : 0, &p, ws_bytes,
+                            &route, &slices),
+           "gtp_sample_route");
+  return {route, slices};
 }
 
 const void* targets_ptr(const at::Tensor& logits, const at::Tensor& targets, int64_t N,
@@ -533,6 +560,10 @@ TORCH_LIBRARY(graspo_tokpath, m) {
       "Tensor? history, Tensor? allow_mask, Tensor? uniforms, Tensor? finished, int pad_token_id, "
       "int stream) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)",
       &sample);
+  m.def(
+      "sample_route(Tensor logits, float temperature, int top_k, float top_p, "
+      "float repetition_penalty, int hist_len, bool has_mask) -> (int, int)",
+      &sample_route);
   m.def("logprob_entropy(Tensor logits, Tensor targets, int stream) -> (Tensor, Tensor, Tensor)",
         &logprob_entropy);
   m.def(

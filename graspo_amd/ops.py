@@ -95,6 +95,23 @@ def sample(
     return SampleOutput(*out)
 
 
+ROUTES = {1: "split top-k", 2: "split top-p", 3: "top-p", 4: "fp32 top-p",
+          5: "value histogram", 6: "row-wise"}
+ROUTE_SPLIT_TOPK, ROUTE_TOPP_SPLIT, ROUTE_TOPP, ROUTE_TOPP32, ROUTE_HIST, ROUTE_ROWWISE = range(1, 7)
+
+
+def sample_route(logits: torch.Tensor, *, temperature: float, top_k: int = 0,
+                 top_p: float = 1.0, repetition_penalty: float = 1.0, hist_len: int = 0,
+                 has_mask: bool = False) -> tuple[int, int]:
+    """(ROUTE_*, workgroups per row) of the kernel :func:`sample` would run for
+    these logits and parameters (gtp_sample_route, with the workspace the op
+    passes).  Host-only: launches nothing."""
+    ops = load()
+    logits = _as_rows(logits)
+    return tuple(ops.sample_route(logits, float(temperature), int(top_k), float(top_p),
+                                  float(repetition_penalty), int(hist_len), bool(has_mask)))
+
+
 def logprob_entropy(logits: torch.Tensor, targets: torch.Tensor):
     """(logprob, entropy, status) per row of ``logits`` [N, V]; one HBM read."""
     ops = load()

@@ -19,12 +19,10 @@ from . import ops
 
 def _fp32_top_p_kernel_takes(logits: torch.Tensor, temperature: float, top_k: int,
                              top_p: float) -> bool:
-    """Whether an fp32 call goes to the fp32 top-p kernel: top-p alone on
-    16-byte aligned rows of 65536 <= V <= 2^18, 0 < T <= 1024."""
-    B, V = logits.shape
-    return (0.0 < top_p < 1.0 and (top_k <= 0 or top_k >= V) and 65536 <= V <= (1 << 18)
-            and temperature <= 1024.0 and logits.data_ptr() % 16 == 0
-            and (logits.stride(0) * 4) % 16 == 0 and logits.stride(1) == 1)
+    """Whether an fp32 call without history or mask goes to the fp32 top-p
+    kernel, as the library's own routing decides (gtp_sample_route)."""
+    route, _ = ops.sample_route(logits, temperature=temperature, top_k=top_k, top_p=top_p)
+    return route == ops.ROUTE_TOPP32
 
 
 def _bf16_when_exact(logits: torch.Tensor, temperature: float, top_k: int,

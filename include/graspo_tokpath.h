@@ -157,6 +157,28 @@ int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
 size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                   const gtp_sampler_params* params);
 
+/*
+ * gtp_sample_route -- which kernel gtp_sample_rows would run for a call, and
+ * how many workgroups split each row; no counterpart in the reference (the
+ * kernels are this library's).  For callers that choose an input format by
+ * the kernel it reaches (the Python drop-in narrows fp32 rows to bf16 unless
+ * the fp32 top-p kernel takes them) and for tests.
+ *   aligned          nonzero when logits and row stride are 16-byte aligned
+ *   hist_len         history entries per row (0: no history)
+ *   has_mask         nonzero when an allow mask is passed
+ *   workspace_bytes  the workspace the call would pass (0: none)
+ * out_route gets one of GTP_ROUTE_*, out_slices the workgroups per row.
+ */
+#define GTP_ROUTE_SPLIT_TOPK 1  /* greedy / top-k <= 128: split sampler      */
+#define GTP_ROUTE_TOPP_SPLIT 2  /* bf16 top-p rows of small batches, split   */
+#define GTP_ROUTE_TOPP 3        /* bf16 top-p rows, one workgroup per row    */
+#define GTP_ROUTE_TOPP32 4      /* fp32 top-p rows, one workgroup per row    */
+#define GTP_ROUTE_HIST 5        /* bf16 value-histogram sampler              */
+#define GTP_ROUTE_ROWWISE 6     /* row-wise sampler (every other call)       */
+int gtp_sample_route(int dtype, int64_t B, int64_t V, int aligned, int64_t hist_len,
+                     int has_mask, const gtp_sampler_params* params, size_t workspace_bytes,
+                     int32_t* out_route, int32_t* out_slices);
+
 /* Size of the library's own workspace for gtp_sample_rows_noalloc. */
 #define GTP_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 

@@ -36,7 +36,28 @@ def lib() -> ctypes.CDLL:
     L.gtp_decode_update_rows.argtypes = [VP, VP, I64, I64, I64, VP, VP, I64, VP, I64, I64, VP,
                                          VP]
     L.gtp_decode_update_rows.restype = I32
+    L.gtp_sample_route.argtypes = [I32, I64, I64, I32, I64, I32, ctypes.POINTER(SamplerParams),
+                                   SZ, ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.POINTER(ctypes.c_int32)]
+    L.gtp_sample_route.restype = I32
     return L
+
+
+ROUTE_SPLIT_TOPK, ROUTE_TOPP_SPLIT, ROUTE_TOPP, ROUTE_TOPP32, ROUTE_HIST, ROUTE_ROWWISE = range(1, 7)
+NOALLOC_SCRATCH_BYTES = 8 << 20
+
+
+def route(L, dtype, B, V, *, T, k=0, P=1.0, rho=1.0, hist_len=0, mask=False, aligned=True,
+          workspace=None):
+    """(route, slices) from gtp_sample_route; workspace None: the bytes
+    gtp_sample_workspace_bytes asks for (what the torch op passes)."""
+    p = SamplerParams(T, k, P, rho)
+    ws = L.gtp_sample_workspace_bytes(dtype, B, V, ctypes.byref(p)) if workspace is None else workspace
+    r, s = ctypes.c_int32(0), ctypes.c_int32(0)
+    rc = L.gtp_sample_route(dtype, B, V, int(aligned), hist_len, int(mask), ctypes.byref(p), ws,
+                            ctypes.byref(r), ctypes.byref(s))
+    assert rc == 0
+    return r.value, s.value
 
 
 DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}

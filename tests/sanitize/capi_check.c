@@ -46,6 +46,19 @@ int main(void) {
   const gtp_sampler_params topp = {0.7f, 0, 0.9f, 1.0f};
 
   /* the workspace query: zero for every call that cannot run */
+  {
+    int32_t rt = 0, sl = 0;
+    EXPECT_RC(w, gtp_sample_route(1, 4, 151936, 1, 0, 0, NULL, 0, &rt, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(1, 4, 151936, 1, 0, 0, &topp, 0, NULL, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(1, 0, 151936, 1, 0, 0, &topp, 0, &rt, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(1, 4, 0, 1, 0, 0, &topp, 0, &rt, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(1, 4, 151936, 1, -1, 0, &topp, 0, &rt, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(7, 4, 151936, 1, 0, 0, &topp, 0, &rt, &sl), I);
+    EXPECT_RC(w, gtp_sample_route(1, 4, INT64_MAX, 1, 0, 0, &topp, 0, &rt, &sl), X);
+    EXPECT_RC(w, gtp_sample_route(1, INT64_MAX, 151936, 1, 0, 0, &topp, 0, &rt, &sl), X);
+    EXPECT_RC(w, gtp_sample_route(1, 4, 151936, 1, 0, 0, &topp, SIZE_MAX, &rt, NULL), OK);
+    EXPECT_RC(w, rt, GTP_ROUTE_TOPP_SPLIT);
+  }
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 4, 100, NULL), 0);
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 0, 151936, &topp), 0);
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 4, 0, &topp), 0);

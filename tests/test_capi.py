@@ -37,6 +37,38 @@ def test_library_exports_every_declared_symbol():
     assert b"gfx950" in lib.gtp_version()
 
 
+def test_sample_route_on_the_host():
+    """gtp_sample_route (host-only; without a GPU the library plans for 256
+    compute units) names the kernel each call shape takes: the split top-k
+    sampler, the split and one-workgroup bf16 top-p kernels, the fp32 top-p
+    kernel, the value-histogram kernel and the row-wise kernel."""
+    from tests import _capi
+
+    L = _capi.lib()
+    F32, BF16, F16 = 0, 1, 2
+    R = _capi
+    assert R.route(L, BF16, 256, 248320, T=0.7, k=64, P=0.9, rho=1.05, hist_len=4096,
+                   mask=True) == (R.ROUTE_SPLIT_TOPK, 1)
+    assert R.route(L, F32, 8, 151936, T=0.7, k=50, P=0.9) == (R.ROUTE_SPLIT_TOPK, 8)
+    assert R.route(L, BF16, 64, 151936, T=1.0, P=0.95, rho=1.1,
+                   hist_len=2048) == (R.ROUTE_TOPP_SPLIT, 4)
+    assert R.route(L, BF16, 64, 151936, T=0.8, P=0.9, mask=True) == (R.ROUTE_TOPP, 1)
+    assert R.route(L, BF16, 256, 248320, T=0.7, P=0.9) == (R.ROUTE_TOPP, 1)
+    assert R.route(L, F32, 256, 248320, T=0.7, P=0.9) == (R.ROUTE_TOPP32, 1)
+    # without a workspace the top-p kernels (hand-over list) are out
+    assert R.route(L, F32, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_ROWWISE, 1)
+    assert R.route(L, BF16, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_HIST, 1)
+    # the allocation-free entry point's 8 MiB array: 7 slices for 16 decode rows
+    assert R.route(L, BF16, 16, 248320, T=0.7, P=0.9)[0] == R.ROUTE_TOPP_SPLIT
+    assert R.route(L, BF16, 16, 248320, T=0.7, P=0.9,
+                   workspace=R.NOALLOC_SCRATCH_BYTES) == (R.ROUTE_TOPP_SPLIT, 7)
+    assert R.route(L, BF16, 4, 60000, T=1.0, P=0.9) == (R.ROUTE_HIST, 1)   # V < 65536
+    assert R.route(L, BF16, 4, 70000, T=1.0, k=300) == (R.ROUTE_HIST, 1)   # top-k > 128
+    assert R.route(L, F16, 4, 70000, T=1.0, P=0.9) == (R.ROUTE_ROWWISE, 1)
+    assert R.route(L, BF16, 4, 70000, T=1.0, k=5, aligned=False)[0] == R.ROUTE_ROWWISE
+    assert R.route(L, BF16, 4, 70000, T=0.0, aligned=True)[0] == R.ROUTE_SPLIT_TOPK
+
+
 def test_invalid_arguments_rejected_before_launch():
     lib = ctypes.CDLL(graspo_amd.LIB_PATH)
     vp, i64 = ctypes.c_void_p, ctypes.c_int64

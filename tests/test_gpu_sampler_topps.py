@@ -125,6 +125,9 @@ def test_noalloc_entry_point_uses_fewer_slices():
     kw = dict(temperature=0.7, top_p=0.9, uniforms=wl.uniforms.to(dev))
     args, p, B = _capi.sample_args(x, **kw)
     assert L.gtp_sample_workspace_bytes(1, B, x.shape[1], ctypes.byref(p)) > 8 << 20
+    # the plan of this call: the split top-p kernel, 7 workgroups per row
+    assert _capi.route(L, 1, B, x.shape[1], T=0.7, P=0.9,
+                       workspace=_capi.NOALLOC_SCRATCH_BYTES) == (_capi.ROUTE_TOPP_SPLIT, 7)
     out = _capi.SampleBuffers(B, dev)
     assert L.gtp_sample_rows_noalloc(*args, *out.out_args(), _capi.stream_handle()) == 0
     torch.cuda.synchronize()
