@@ -13,11 +13,14 @@
  *
  * Conventions shared by every entry point:
  *   - All array pointers are DEVICE pointers owned by the caller.  The library
- *     never allocates and is reentrant.  Its only mutable global state is:
- *     the measurement hook's per-thread event pair (gtp_time_next_launch);
- *     a per-device cache of the compute-unit count, filled once per device
- *     with atomic stores; and the per-device scratch array of
- *     gtp_sample_rows_noalloc with its per-device address table.
+ *     never allocates and is reentrant, with one exception:
+ *     gtp_sample_rows_noalloc works in one library-owned array per GPU, so
+ *     two of its calls that overlap on one GPU (different streams or host
+ *     threads) race; the caller serialises them.  The library's only mutable
+ *     global state is: the measurement hook's per-thread event pair
+ *     (gtp_time_next_launch); a per-device cache of the compute-unit count,
+ *     filled once per device with atomic stores; and that per-device array
+ *     with its per-device address table.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL is the default stream).
  *   - Return value: GTP_OK or a GTP_ERR_* code for a bad argument or a failed
