@@ -6,7 +6,10 @@ the sampler over a bf16 [256, 248320] batch (repetition penalty over a
 one logprob/entropy pass over bf16 [8192, 248320] with int32 targets.
 Inputs are generated on the GPU and resident in HBM before timing; two
 sampler batches alternate and the 4 GB logprob pass between them evicts the
-256 MB MALL, so every sampler launch reads its logits from HBM.
+256 MB MALL, so every sampler launch reads its logits from HBM.  In a timed
+step each kernel runs alone: the host waits for the GPU to drain before
+each launch, so that no kernel shares the GPU with the last workgroups of
+the one before it.
 
 Prints ONE JSON line.  ``value`` is sampled rows/s of the sampler kernel;
 ``logprob_tokens_per_s`` is the logprob kernel's throughput.  Kernel times
@@ -14,8 +17,12 @@ come from HIP events on the stream the kernels are launched on (torch's
 current stream, which the ops use), recorded at each kernel's own dispatch
 start and end through the library's launch hook (gtp_time_next_launch,
 hipExtLaunchKernelGGL), as rocprofv3 times a kernel.  Events recorded around
-a launch also count the event packets' idle microseconds; those figures are
-reported beside as ``avg_us_events_around_launch``.
+a launch also count the event packets' idle microseconds and, the GPU being
+drained before each timed launch, the host's launch latency; those figures
+are reported beside as ``avg_us_events_around_launch``.  The side
+measurements below run before the timed steps, and the step itself runs
+untimed for PREWARM_S seconds before the W warm-up steps (reported as
+``prewarm``), so that the timed steps run at the GPU's steady state.
 
 ``rooflines.logprob_backward`` times the logprob gradient kernel over the
 same [8192, 248320] logits (read once, bf16 gradient written once).
@@ -34,8 +41,10 @@ expression, with the bf16 GEMM's TFLOP/s against the matrix-core peak.
 ``per_config`` adds the other sampler workloads (fp32 [8,151936]; bf16
 [64,151936] top-p only; bf16 [64,151936] masked; the [256,248320] rows with
 top-p only -- the decode loop's T 0.7 / P 0.9 rows, and the same with the
-history and mask -- on the top-p kernel), each timed alone with a 512 MB
-buffer written between launches to evict the MALL, and the loss-side
+history and mask -- on the top-p kernel), each call timed alone (a
+read-only pass over a 512 MB buffer evicts the MALL and the GPU drains
+before every launch; a top-p call's time spans its kernel and the hand-over
+kernel), and the loss-side
 logprob workload: bf16 [32768,151936] x 2 passes (policy and reference
 logits) in 4 chunks of 8192 rows each.
 
@@ -61,6 +70,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+PREWARM_S = 0.3  # seconds of untimed steps before the warm-up steps
 REPO = os.path.dirname(os.path.abspath(__file__))
 SAMPLER_KERNEL = "sampler_split_kernel<bf16>"
 LOGPROB_KERNEL = "logprob_entropy_kernel<bf16>"
@@ -205,6 +215,19 @@ def kernel_events(n: int):
     return evs
 
 
+def evict(flush) -> None:
+    """Evicts the 256 MB last-level cache (MALL) with a read-only pass over a
+    512 MB buffer, then waits for the GPU to drain: the next kernel starts
+    cold, alone on the GPU, with no dirty lines to write back (an in-place
+    write pass instead leaves 512 MB dirty, and the next kernel pays for
+    their write-back: the configuration-5 sampler measured 41 against
+    37.6 us)."""
+    import torch
+
+    flush.amax()
+    torch.cuda.synchronize()
+
+
 def stream_floor_us(x, flush, iters: int = 10) -> float:
     """Average kernel time of gtp_stream_read_rows over the rows of ``x``
     (a read-only pass with the samplers' access pattern), MALL evicted
@@ -229,7 +252,7 @@ def stream_floor_us(x, flush, iters: int = 10) -> float:
         assert fn(*args) == 0
     evs = kernel_events(iters)
     for e0, e1 in evs:
-        flush.add_(1)
+        evict(flush)
         ops.time_next_launch(e0, e1)
         assert fn(*args) == 0
     torch.cuda.synchronize()
@@ -259,7 +282,7 @@ def time_sampler_config(cfg: int, dev, iters: int, flush, kernel: str = SAMPLER_
         ops.sample(wl.logits, **kw)
     evs = kernel_events(iters)
     for e0, e1 in evs:
-        flush.add_(1)
+        evict(flush)
         ops.time_next_launch(e0, e1)
         ops.sample(wl.logits, **kw)
     torch.cuda.synchronize()
@@ -573,23 +596,72 @@ def main() -> int:
 
     def step(i, evs=None):
         # evs: events around the two launches (0-2) and, through the launch
-        # hook, at each kernel's own start and end (3-4 sampler, 5-6 logprob)
+        # hook, at each kernel's own start and end (3-4 sampler, 5-6 logprob).
+        # Timed steps wait for the GPU to drain before each launch, so that a
+        # kernel never shares the GPU with the last workgroups of the one
+        # before it (the sampler right behind the logprob pass measured 43.2
+        # us that way, 37.6 us alone); the logprob pass of the previous step
+        # has evicted the sampler's rows from the MALL with reads only.
         w = batches[i % 2]
         if evs:
+            torch.cuda.synchronize()
             evs[0].record()
             ops.time_next_launch(evs[3], evs[4])
         ops.sample(w.logits, **w.kwargs())
         if evs:
             evs[1].record()
+            torch.cuda.synchronize()
+            evs[7].record()
             ops.time_next_launch(evs[5], evs[6])
         ops.logprob_entropy(lx, lt)
         if evs:
             evs[2].record()
 
+    # The side measurements run first: about a second of GPU work, after
+    # which the GPU runs at its steady-state clocks (a cold GPU ran the
+    # sampler's first timed steps at 56 us, settling to ~37 us over 20 steps).
+    side = {}
+    # the gradient of the logprob pass (one read of the logits, one write of
+    # the bf16 gradient), the kernel behind the autograd backward
+    g_lp = torch.randn(N, device=dev)
+    lp_f, _, _ = ops.logprob_entropy(lx, lt)
+    lse = lx.gather(1, lt.long().unsqueeze(1)).squeeze(1).float() - lp_f
+    grad = torch.empty_like(lx)
+    for _ in range(2):
+        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
+    bevs = kernel_events(10)
+    for e0, e1 in bevs:
+        ops.time_next_launch(e0, e1)
+        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
+    torch.cuda.synchronize()
+    b_ms = sum(a.elapsed_time(b) for a, b in bevs) / len(bevs)
+    b_bytes = 2 * N * V * lx.element_size() + N * (lt.element_size() + 4 + 4)
+    b_gbs = b_bytes / (b_ms * 1e-3) / 1e9
+    side["logprob_backward"] = {
+        "bound": "hbm", "achieved": round(b_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(b_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(BACKWARD_KERNEL),
+        "kernel": BACKWARD_KERNEL, "algorithmic_bytes": b_bytes, "avg_us": round(b_ms * 1e3, 2)}
+    del grad, g_lp, lse, lp_f
+    side["graspo_loss"] = time_graspo_loss(dev)
+    side["decode_loop"] = time_decode_loop(dev)
+    side["hidden_logprobs"] = time_hidden_logprobs(dev)
+    # the step itself, untimed, for PREWARM_S before the W warm-up steps: a
+    # GPU coming from other work or from idle ran the sampler's first steps
+    # at 48-58 us, settling at ~37 us only after some tens of steps of this
+    # same loop
+    prewarm_steps, t_pw = 0, time.perf_counter()
+    while time.perf_counter() - t_pw < PREWARM_S:
+        step(prewarm_steps)
+        prewarm_steps += 1
+        if prewarm_steps % 32 == 0:
+            torch.cuda.synchronize()
     for i in range(args.warmup):
         step(i)
+    # per step: events around the sampler launch (0, 1) and after the logprob
+    # launch (2), the hook's pairs (3-4, 5-6), and before the logprob launch (7)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
-              + [e for pair in kernel_events(2) for e in pair] for _ in range(args.steps)]
+              + [e for pair in kernel_events(2) for e in pair]
+              + [torch.cuda.Event(enable_timing=True)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -597,11 +669,12 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     # kernel time: the events the launch hook records at each kernel's own
-    # dispatch; around the launches, event packets add a few idle microseconds
+    # dispatch; events recorded around a launch on the drained GPU also count
+    # the host's launch latency
     s_ms = sum(e[3].elapsed_time(e[4]) for e in events) / args.steps
     l_ms = sum(e[5].elapsed_time(e[6]) for e in events) / args.steps
     s_ev_us = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps * 1e3
-    l_ev_us = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps * 1e3
+    l_ev_us = sum(e[7].elapsed_time(e[2]) for e in events) / args.steps * 1e3
 
     s_bytes = wl.algorithmic_bytes()
     l_bytes = W.logprob_algorithmic_bytes(N, V, lx.element_size())
@@ -635,36 +708,19 @@ def main() -> int:
             "sampler_batch": B, "vocab": V, "logprob_rows": N, "input_dtype": "bf16",
             "parallelism": "single-gpu",
         },
+        "prewarm": {"seconds": PREWARM_S, "steps": prewarm_steps,
+                    "what": "the step run untimed before the warm-up steps, so that the "
+                            "timed steps run at the GPU's steady state"},
         "logprob_tokens_per_s": round(N / (l_ms * 1e-3), 1),
         "roofline": dominant,
         "rooflines": {"sampler": roof_s, "logprob": roof_l},
         "per_config": None,
         "cpu_baseline": None,
     }
-    # the gradient of the logprob pass (one read of the logits, one write of
-    # the bf16 gradient), the kernel behind the autograd backward
-    g_lp = torch.randn(N, device=dev)
-    lp_f, _, _ = ops.logprob_entropy(lx, lt)
-    lse = lx.gather(1, lt.long().unsqueeze(1)).squeeze(1).float() - lp_f
-    grad = torch.empty_like(lx)
-    for _ in range(2):
-        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
-    bevs = kernel_events(10)
-    for e0, e1 in bevs:
-        ops.time_next_launch(e0, e1)
-        ops.logprob_backward(lx, lt, g_lp, lse, out=grad)
-    torch.cuda.synchronize()
-    b_ms = sum(a.elapsed_time(b) for a, b in bevs) / len(bevs)
-    b_bytes = 2 * N * V * lx.element_size() + N * (lt.element_size() + 4 + 4)
-    b_gbs = b_bytes / (b_ms * 1e-3) / 1e9
-    line["rooflines"]["logprob_backward"] = {
-        "bound": "hbm", "achieved": round(b_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(b_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(BACKWARD_KERNEL),
-        "kernel": BACKWARD_KERNEL, "algorithmic_bytes": b_bytes, "avg_us": round(b_ms * 1e3, 2)}
-    del lx, lt, batches, wl_b, grad, g_lp, lse, lp_f
-    line["graspo_loss"] = time_graspo_loss(dev)
-    line["decode_loop"] = time_decode_loop(dev)
-    line["hidden_logprobs"] = time_hidden_logprobs(dev)
+    line["rooflines"]["logprob_backward"] = side["logprob_backward"]
+    for k in ("graspo_loss", "decode_loop", "hidden_logprobs"):
+        line[k] = side[k]
+    del lx, lt, batches, wl_b
     flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)  # 512 MB
     roof_s["stream_floor_us"] = round(stream_floor_us(wl.logits, flush), 2)
     if not args.no_per_config:
