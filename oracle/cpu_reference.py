@@ -27,13 +27,16 @@ import torch
 def penalised(x, history, repetition_penalty):
     """HF's ``RepetitionPenaltyLogitsProcessor`` rule (x < 0 ? x*rho : x/rho)
     once per distinct history id of each row; ids < 0 are padding and
-    penalise nothing."""
+    penalise nothing.  Every copy of a repeated id writes the same value,
+    computed from the unpenalised logit."""
     h = history.long()
     valid = (h >= 0) & (h < x.shape[1])
-    hits = torch.zeros(x.shape, dtype=torch.int32)
-    hits.scatter_add_(1, torch.where(valid, h, 0), valid.to(torch.int32))
-    pen = torch.where(x < 0, x * repetition_penalty, x / repetition_penalty)
-    return torch.where(hits > 0, pen, x)
+    vals = x.gather(1, torch.where(valid, h, 0))
+    pen = torch.where(vals < 0, vals * repetition_penalty, vals / repetition_penalty)
+    rows = torch.arange(x.shape[0]).unsqueeze(1).expand_as(h)
+    out = x.clone()
+    out[rows[valid], h[valid]] = pen[valid]
+    return out
 
 
 def sample_rows(logits, *, temperature, top_k=0, top_p=1.0, repetition_penalty=1.0,
@@ -46,9 +49,23 @@ def sample_rows(logits, *, temperature, top_k=0, top_p=1.0, repetition_penalty=1
     if temperature <= 0:
         return x.argmax(dim=-1)
     x = x / max(float(temperature), 1e-6)
-    ys, sorted_idx = torch.sort(x, dim=-1, descending=True, stable=True)
-    if top_k > 0:
-        ys[:, top_k:] = float("-inf")
+    if 0 < top_k < x.shape[1]:
+        # exactly k tokens: every one above the k-th value, then the tokens
+        # equal to it by ascending id; only those k are sorted.  torch.topk
+        # keeps an arbitrary subset of a tie at the k-th value, so a row
+        # whose tie is split takes its lowest ids instead.
+        vals, cand = torch.topk(x, top_k, dim=-1)
+        kth = vals[:, -1:]
+        split = (x == kth).sum(dim=-1) != (vals == kth).sum(dim=-1)
+        for b in split.nonzero().flatten().tolist():
+            above = (x[b] > kth[b]).nonzero().flatten()
+            ties = (x[b] == kth[b]).nonzero().flatten()[: top_k - above.numel()]
+            cand[b] = torch.cat([above, ties])
+        cand, _ = torch.sort(cand, dim=-1)  # ascending ids: the stable sort's tie order
+        ys, order = torch.sort(x.gather(1, cand), dim=-1, descending=True, stable=True)
+        sorted_idx = cand.gather(1, order)
+    else:
+        ys, sorted_idx = torch.sort(x, dim=-1, descending=True, stable=True)
     sorted_probs = torch.softmax(ys, dim=-1)
     if 0.0 < top_p < 1.0:
         cum = torch.cumsum(sorted_probs, dim=-1)
