@@ -499,26 +499,119 @@ __global__ __launch_bounds__(256) void softmax_grad_bf16_cols_kernel(
   }
 }
 
+// The same values written token-major as well, grad_n[n, v] (and, unless
+// grad_t is null, vocabulary-major as above), from one read of the logits: a
+// workgroup takes 256 tokens x 64 vocabulary rows.  Each thread computes 4
+// consecutive tokens of 16 rows (16-byte loads along the tokens, 8-byte
+// vocabulary-major stores) and puts them in an LDS tile [64][256 + 2]; then
+// each group of 8 lanes writes one token's 64 values, a whole 128-byte line,
+// 16 bytes a lane.  The tile's row pitch of 129 words puts the 8 rows a group
+// reads at once on distinct banks.
+constexpr int kDgTok = 256, kDgRows = 64, kDgPitch = kDgTok + 2;
+__global__ __launch_bounds__(256) void softmax_grad_bf16_dual_kernel(
+    const float* __restrict__ logits_t, int64_t V, int64_t N, int64_t ld,
+    const float* __restrict__ grad_lp, const float* __restrict__ lse_in,
+    uint16_t* __restrict__ grad_t, int64_t gld, uint16_t* __restrict__ grad_n, int64_t nld,
+    int vec) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kDgRows * kDgPitch];
+  const int t = threadIdx.x;
+  const int64_t nb = (int64_t)blockIdx.x * kDgTok, vb = (int64_t)blockIdx.y * kDgRows;
+  const int nl = (t & 63) * 4;  // the thread's first token in the tile
+  const int64_t n0 = nb + nl;
+  const int cnt = (int)max((int64_t)0, min((int64_t)4, N - n0));
+  float ng[4], c[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float g = j < cnt ? grad_lp[n0 + j] : 0.0f;
+    ng[j] = -g;
+    c[j] = g == 0.0f ? kNegInf : (j < cnt ? lse_in[n0 + j] : 0.0f);
+  }
+  auto grad_of = [&](float x, int j) {
+    return c[j] == kNegInf ? 0.0f : ng[j] * __builtin_amdgcn_exp2f((x - c[j]) * kLog2e);
+  };
+#pragma unroll 4
+  for (int i = 0; i < kDgRows / 4; ++i) {
+    const int r = (t >> 6) + 4 * i;
+    const int64_t v = vb + r;
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+    if (v < V) {
+      if (vec && cnt == 4) {
+        const f32x4v x = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(logits_t + v * ld + n0));
+        o[0] = bf16_rne(grad_of(x.x, 0));
+        o[1] = bf16_rne(grad_of(x.y, 1));
+        o[2] = bf16_rne(grad_of(x.z, 2));
+        o[3] = bf16_rne(grad_of(x.w, 3));
+        if (grad_t) {
+          const u32x2 w = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+          __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(grad_t + v * gld + n0));
+        }
+      } else {
+        for (int j = 0; j < cnt; ++j) {
+          o[j] = bf16_rne(grad_of(logits_t[v * ld + n0 + j], j));
+          if (grad_t) grad_t[v * gld + n0 + j] = (uint16_t)o[j];
+        }
+      }
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(tile + r * kDgPitch + nl);
+    dst[0] = o[0] | (o[1] << 16);
+    dst[1] = o[2] | (o[3] << 16);
+  }
+  __syncthreads();
+  // token-major: 8 lanes per token, lane c8 of the group the values of rows
+  // 8 c8 .. 8 c8 + 7, 32 tokens per pass
+  const int c8 = t & 7;
+  const int64_t nv = min((int64_t)kDgRows, V - vb);
+#pragma unroll 2
+  for (int p = 0; p < kDgTok / 32; ++p) {
+    const int tl = p * 32 + (t >> 3);
+    const int64_t n = nb + tl;
+    if (n >= N) break;
+    uint16_t* row = grad_n + n * nld + vb;
+    if (vec && nv == kDgRows) {
+      uint32_t h[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) h[k] = tile[(8 * c8 + k) * kDgPitch + tl];
+      const u32x4 w = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                       h[6] | (h[7] << 16)};
+      *reinterpret_cast<u32x4*>(row + 8 * c8) = w;
+    } else {
+      for (int k = 0; k < 8; ++k)
+        if (8 * c8 + k < nv) row[8 * c8 + k] = tile[(8 * c8 + k) * kDgPitch + tl];
+    }
+  }
+}
+
 extern "C" int gtp_softmax_grad_bf16_cols(const float* logits_t, int64_t V, int64_t N,
                                           int64_t logits_stride, const float* grad_logprob,
                                           const float* lse, uint16_t* grad_t, int64_t grad_stride,
+                                          uint16_t* grad_n, int64_t grad_n_stride,
                                           void* stream) {
-  if (N < 0 || V <= 0 || logits_stride < N || grad_stride < N ||
-      (N > 0 && (!logits_t || !grad_logprob || !lse || !grad_t)))
+  if (N < 0 || V <= 0 || logits_stride < N || (grad_t && grad_stride < N) ||
+      (grad_n && grad_n_stride < V) ||
+      (N > 0 && (!logits_t || !grad_logprob || !lse || (!grad_t && !grad_n))))
     return GTP_ERR_INVALID_ARGUMENT;
   if (N > 0x7FFFFFFFll || V > ((int64_t)65535 * kSgRows) ||
-      logits_stride > ((int64_t)1 << 40) / V || grad_stride > ((int64_t)1 << 40) / V)
+      logits_stride > ((int64_t)1 << 40) / V || (grad_t && grad_stride > ((int64_t)1 << 40) / V) ||
+      (grad_n && (N > 0 && grad_n_stride > ((int64_t)1 << 40) / N)))
     return GTP_ERR_UNSUPPORTED;
   if (N == 0) return GTP_OK;
-  const int vec = ((reinterpret_cast<uintptr_t>(logits_t) & 15u) == 0 &&
-                   (reinterpret_cast<uintptr_t>(grad_t) & 7u) == 0 && (logits_stride & 3) == 0 &&
-                   (grad_stride & 3) == 0)
-                      ? 1
-                      : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)((N + 1023) / 1024), (unsigned)((V + kSgRows - 1) / kSgRows));
-  launch_timed(softmax_grad_bf16_cols_kernel, grid, dim3(256), s, logits_t, V, N, logits_stride,
-               grad_logprob, lse, grad_t, grad_stride, vec);
+  const bool in_vec = (reinterpret_cast<uintptr_t>(logits_t) & 15u) == 0 && (logits_stride & 3) == 0;
+  const bool t_vec = !grad_t || ((reinterpret_cast<uintptr_t>(grad_t) & 7u) == 0 && (grad_stride & 3) == 0);
+  if (grad_n) {
+    const int vec = in_vec && t_vec && (reinterpret_cast<uintptr_t>(grad_n) & 15u) == 0 &&
+                            (grad_n_stride & 7) == 0
+                        ? 1
+                        : 0;
+    const dim3 grid((unsigned)((N + kDgTok - 1) / kDgTok), (unsigned)((V + kDgRows - 1) / kDgRows));
+    launch_timed(softmax_grad_bf16_dual_kernel, grid, dim3(256), s, logits_t, V, N, logits_stride,
+                 grad_logprob, lse, grad_t, grad_stride, grad_n, grad_n_stride, vec);
+  } else {
+    const int vec = in_vec && t_vec ? 1 : 0;
+    const dim3 grid((unsigned)((N + 1023) / 1024), (unsigned)((V + kSgRows - 1) / kSgRows));
+    launch_timed(softmax_grad_bf16_cols_kernel, grid, dim3(256), s, logits_t, V, N, logits_stride,
+                 grad_logprob, lse, grad_t, grad_stride, vec);
+  }
   return hipGetLastError() == hipSuccess ? GTP_OK : GTP_ERR_LAUNCH;
 }
 

@@ -529,9 +529,13 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> lm_head_logprob_save(
 }
 
 // bf16(-g * softmax) of vocabulary-major fp32 logits [V, N] (row stride
-// free, unit column stride), g and lse fp32 [N]; returns [V, N] bf16
-at::Tensor softmax_grad_bf16(const at::Tensor& logits_t, const at::Tensor& grad_logprob,
-                             const at::Tensor& lse, int64_t stream) {
+// free, unit column stride), g and lse fp32 [N]; returns ([V, N] bf16 or an
+// empty tensor, [N, V] bf16 or an empty tensor) as `layouts` asks (1:
+// vocabulary-major, 2: token-major, 3: both)
+std::tuple<at::Tensor, at::Tensor> softmax_grad_bf16(const at::Tensor& logits_t,
+                                                     const at::Tensor& grad_logprob,
+                                                     const at::Tensor& lse, int64_t layouts,
+                                                     int64_t stream) {
   TORCH_CHECK(logits_t.is_cuda() && logits_t.scalar_type() == at::kFloat && logits_t.dim() == 2 &&
                   (logits_t.size(1) <= 1 || logits_t.stride(1) == 1),
               "graspo_tokpath.softmax_grad_bf16: logits_t must be a float32 [V, N] GPU tensor "
@@ -543,15 +547,19 @@ at::Tensor softmax_grad_bf16(const at::Tensor& logits_t, const at::Tensor& grad_
                   grad_logprob.is_contiguous() && lse.scalar_type() == at::kFloat &&
                   lse.numel() == N && lse.is_contiguous(),
               "graspo_tokpath.softmax_grad_bf16: grad_logprob and lse must be float32 [N]");
-  at::Tensor out = at::empty({V, N}, logits_t.options().dtype(at::kBFloat16));
-  if (V == 0 || N == 0) return out;
+  TORCH_CHECK(layouts >= 1 && layouts <= 3, "graspo_tokpath.softmax_grad_bf16: layouts must be 1, 2 or 3");
+  const auto bf = logits_t.options().dtype(at::kBFloat16);
+  at::Tensor out_t = (layouts & 1) ? at::empty({V, N}, bf) : at::empty({0}, bf);
+  at::Tensor out_n = (layouts & 2) ? at::empty({N, V}, bf) : at::empty({0}, bf);
+  if (V == 0 || N == 0) return {out_t, out_n};
   const int64_t ld = V > 1 ? logits_t.stride(0) : N;
   const int rc = gtp_softmax_grad_bf16_cols(
       logits_t.data_ptr<float>(), V, N, ld, grad_logprob.data_ptr<float>(),
-      lse.data_ptr<float>(), static_cast<uint16_t*>(out.data_ptr()), N,
+      lse.data_ptr<float>(), (layouts & 1) ? static_cast<uint16_t*>(out_t.data_ptr()) : nullptr,
+      N, (layouts & 2) ? static_cast<uint16_t*>(out_n.data_ptr()) : nullptr, V,
       reinterpret_cast<void*>(stream));
   check_rc(rc, "gtp_softmax_grad_bf16_cols");
-  return out;
+  return {out_t, out_n};
 }
 
 TORCH_LIBRARY(graspo_tokpath, m) {
@@ -601,6 +609,6 @@ TORCH_LIBRARY(graspo_tokpath, m) {
   m.def("lm_head_logprob_save(Tensor hidden, Tensor weight, Tensor targets, int stream) -> "
         "(Tensor, Tensor, Tensor, Tensor)",
         &lm_head_logprob_save);
-  m.def("softmax_grad_bf16(Tensor logits_t, Tensor grad_logprob, Tensor lse, int stream) -> Tensor",
+  m.def("softmax_grad_bf16(Tensor logits_t, Tensor grad_logprob, Tensor lse, int layouts, int stream) -> (Tensor, Tensor)",
         &softmax_grad_bf16);
 }

@@ -223,15 +223,21 @@ def lm_head_logprob_save(hidden: torch.Tensor, weight: torch.Tensor, targets: to
     return ops.lm_head_logprob_save(hidden, weight, targets, _stream(hidden))
 
 
-def softmax_grad_bf16(logits_t: torch.Tensor, grad_logprob: torch.Tensor, lse: torch.Tensor):
-    """bf16 [V, N] of -g_n * softmax(logits[n]) for vocabulary-major fp32
-    ``logits_t`` [V, N] (unit column stride; ``lse`` each token's
-    log-sum-exp): the gradient of g * log_softmax(logits)[t] without its
-    one-hot term g * [v == t], transposed."""
+def softmax_grad_bf16(logits_t: torch.Tensor, grad_logprob: torch.Tensor, lse: torch.Tensor,
+                      *, vocab_major: bool = True, token_major: bool = False):
+    """bf16 -g_n * softmax(logits[n]) for vocabulary-major fp32 ``logits_t``
+    [V, N] (unit column stride; ``lse`` each token's log-sum-exp): the
+    gradient of g * log_softmax(logits)[t] without its one-hot term
+    g * [v == t].  Returns ``(grad_t [V, N], grad [N, V])``, each written
+    when asked for (None otherwise), both from one read of the logits."""
+    if not (vocab_major or token_major):
+        raise ValueError("softmax_grad_bf16: ask for at least one layout")
     ops = load()
-    return ops.softmax_grad_bf16(
+    gt, gn = ops.softmax_grad_bf16(
         logits_t, grad_logprob.reshape(-1).to(torch.float32).contiguous(),
-        lse.reshape(-1).to(torch.float32).contiguous(), _stream(logits_t))
+        lse.reshape(-1).to(torch.float32).contiguous(),
+        (1 if vocab_major else 0) | (2 if token_major else 0), _stream(logits_t))
+    return (gt if vocab_major else None), (gn if token_major else None)
 
 
 def decode_update(ids: torch.Tensor, status: torch.Tensor | None, finished: torch.Tensor,

@@ -341,14 +341,18 @@ int gtp_logprob_backward_rows(const void* logits, int dtype, int64_t N,
  * the caller adds in fp32.  Each element is within 2^-8 of -g p.  Feeds the
  * hidden-state path's backward (tensor_utils.py:167-186 under autograd):
  * bf16 matrix-core GEMMs of it against the exact bf16 operands, fp32 output.
+ * With grad_n the same values are also written token-major, from the same
+ * read of the logits (the two gradient GEMMs each run fastest on one of the
+ * two layouts).
  *   logits_t  [V, logits_stride] fp32 (the first N of each row are read)
  *   grad_logprob, lse  [N] fp32; a token with g == 0 gets zeros
- *   grad_t    [V, grad_stride] bf16
+ *   grad_t    [V, grad_stride] bf16, or NULL (then grad_n is required)
+ *   grad_n    [N, grad_n_stride] bf16, or NULL
  */
 int gtp_softmax_grad_bf16_cols(const float* logits_t, int64_t V, int64_t N,
                                int64_t logits_stride, const float* grad_logprob,
                                const float* lse, uint16_t* grad_t, int64_t grad_stride,
-                               void* stream);
+                               uint16_t* grad_n, int64_t grad_n_stride, void* stream);
 
 /*
  * gtp_logprob_backward_split_rows -- the gradient of gtp_logprob_backward_rows

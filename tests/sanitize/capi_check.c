@@ -220,16 +220,20 @@ int main(void) {
   EXPECT_RC(w, gtp_lm_head_logprob_save_rows(NULL, 0, 128, 128, NULL, 1000, 128, NULL, 0, NULL,
                                              NULL, NULL, NULL, NULL, 0, NULL, 0, NULL), OK);
 
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, -1, 10, F, F, h, 10, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 3, F, F, h, 10, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, h, 3, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 0, 4, 4, F, F, h, 4, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, NULL, F, h, 4, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, NULL, 4, NULL), I);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, INT64_MAX, INT64_MAX, F, F, h, INT64_MAX, NULL),
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, -1, 10, F, F, h, 10, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 3, F, F, h, 10, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, h, 3, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 0, 4, 4, F, F, h, 4, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, NULL, F, h, 4, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, NULL, 4, NULL, 0, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, INT64_MAX, INT64_MAX, F, F, h, INT64_MAX, NULL, 0, NULL),
             X);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, INT64_MAX, 4, 4, F, F, h, 4, NULL), X);
-  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(NULL, 10, 0, 0, NULL, NULL, NULL, 0, NULL), OK);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, INT64_MAX, 4, 4, F, F, h, 4, NULL, 0, NULL), X);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(NULL, 10, 0, 0, NULL, NULL, NULL, 0, NULL, 0, NULL), OK);
+  /* the token-major output: its stride must hold V, and bound N * stride */
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, NULL, 0, h, 9, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, h, 4, h, 9, NULL), I);
+  EXPECT_RC(w, gtp_softmax_grad_bf16_cols(F, 10, 4, 4, F, F, NULL, 0, h, INT64_MAX, NULL), X);
 
   EXPECT_RC(w, strstr(gtp_version(), "gfx950") != NULL, 1);
 

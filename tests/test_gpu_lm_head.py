@@ -164,10 +164,20 @@ def test_softmax_grad_bf16(N, V, stride):
     g[min(2, N - 1)] = 0.0
     lse = torch.logsumexp(xt.double(), dim=0).float()
     print("softmax grad:", N, V, stride, flush=True)
-    gs = ops.softmax_grad_bf16(xt, g, lse)
+    gs, none = ops.softmax_grad_bf16(xt, g, lse)
     torch.cuda.synchronize()
+    assert none is None
     assert gs.dtype == torch.bfloat16 and tuple(gs.shape) == (V, N)
     ref = -g.double().unsqueeze(0) * torch.exp(xt.double() - lse.double().unsqueeze(0))
     err = (gs.double() - ref).abs() - (2.0 ** -8 + 1e-5) * ref.abs() - 1e-38
     assert err.max().item() <= 0.0
     assert not bool(gs[:, min(2, N - 1)].float().any())
+    # both layouts from one pass, and the token-major one alone: the same
+    # values bit for bit
+    print("softmax grad, both layouts:", N, V, stride, flush=True)
+    gt2, gn2 = ops.softmax_grad_bf16(xt, g, lse, token_major=True)
+    none, gn3 = ops.softmax_grad_bf16(xt, g, lse, vocab_major=False, token_major=True)
+    torch.cuda.synchronize()
+    assert none is None and tuple(gn2.shape) == (N, V) and tuple(gn3.shape) == (N, V)
+    assert torch.equal(gt2, gs)
+    assert torch.equal(gn2, gs.t()) and torch.equal(gn3, gs.t())
