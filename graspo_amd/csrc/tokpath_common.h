@@ -79,6 +79,33 @@ __device__ __forceinline__ int32_t rank_key_id(uint64_t k) {
 }
 __device__ __forceinline__ float rank_key_y(uint64_t k) { return unord32((uint32_t)(k >> 32)); }
 
+// ------------------------------------------------- division by the temperature
+// x / T rounded to nearest even, the IEEE quotient, for 2^-20 <= T <= 1024,
+// with rT = RN(1 / T) and bh = RN(T 2^-25 (1 - 2^-20)) set once per call.
+// q0 = RN(x rT) lies within 2 ulp of x / T; one correction with its fma
+// residual, q = fma(x - q0 T, rT, q0), is almost always the rounded quotient.
+// The check is exact whatever q is: with q = f 2^e (f in [0.5, 1)) and
+// r = RN(x - q T) (one fma), |r| < bh 2^e gives |x - q T| < T ulp(q) / 2
+// (r's own rounding is inside the 2^-20 margin, and with |q| >= 2^-60 it
+// cannot underflow), so x / T lies strictly within half an ulp of q, and q
+// is the rounded quotient whenever both neighbours of q lie ulp(q) away (q
+// not a power of two).  Infinite or NaN x gives a NaN residual, q = 0 or a
+// power of two fails the mantissa test, tiny q the exponent test: those
+// tokens, and any other that fails (near-ties), take the division.
+__device__ __forceinline__ float div_by_t(float x, float T, float rT, float bh) {
+  const float q0 = x * rT;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, T, x), rT, q0);
+  const float r = __builtin_fmaf(-q, T, x);
+  const int e = __builtin_amdgcn_frexp_expf(q);
+  const bool ok = (__builtin_fabsf(r) < __builtin_ldexpf(bh, e)) & (e >= -59) &
+                  ((f2u(q) & 0x7FFFFFu) != 0u);
+  if (__builtin_expect(ok, 1)) return q;
+  // (the empty asm keeps the division in its own block, off the common path)
+  asm volatile("" ::: "memory");
+  return x / T;
+}
+__host__ __device__ inline float div_by_t_bound(float T) { return T * 0x1p-25f * (1.0f - 0x1p-20f); }
+
 // ------------------------------------------------------------ DETEXP_FIX
 // round(e^d * 2^40) for d <= 0; the step list is the contract written out in
 // include/graspo_tokpath.h and must not be reordered.  The final scaling by

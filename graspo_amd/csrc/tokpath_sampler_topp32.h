@@ -328,6 +328,7 @@ __device__ __forceinline__ bool topp32_row(const SamplerArgs& a, int64_t b, Smem
   const uint32_t last_word = (uint32_t)((V - 1) >> 5);
   const float Tc = a.T > 1e-6f ? a.T : 1e-6f;
   const float rT = 1.0f / Tc;
+  const float bh = div_by_t_bound(Tc);
   const float rho = a.rho;
   // schedule index -> chunk: the first kW start kW evenly spaced regions
   auto perm = [&](uint32_t c) -> uint32_t { return c < per * kW ? (c % kW) * per + c / kW : c; };
@@ -727,7 +728,7 @@ __device__ __forceinline__ bool topp32_row(const SamplerArgs& a, int64_t b, Smem
   auto tok2 = [&](float x, uint32_t id, bool valid, bool al, bool pn) __attribute__((always_inline)) {
     if (raw_again) ls2 += valid ? __builtin_amdgcn_exp2f((x - rx) * kLog2e) : 0.0f;
     const float xp = xpen(x, pn);
-    const float y = xp / Tc;  // (-0 is canonicalised where it is stored)
+    const float y = div_by_t(xp, Tc, rT, bh);  // xp / Tc (-0 is canonicalised where it is stored)
     const float d = fmaxf(al ? y - m : -100.0f, -30.5f);
     const double w = detexp_fix_f64(d);
     wacc += w;

@@ -150,15 +150,17 @@ def test_save_keeps_the_logits(N, V, K):
     assert (lse.double() - rlse).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("N,V,stride", [(4099, 300, 4099), (8192, 2000, 8192), (1000, 77, 1004),
-                                        (3, 5000, 3)])
-def test_softmax_grad_bf16(N, V, stride):
+@pytest.mark.parametrize("N,V,stride,off", [(4099, 300, 4099, 0), (8192, 2000, 8192, 0),
+                                            (1000, 77, 1004, 0), (3, 5000, 3, 0),
+                                            (777, 130, 781, 1)])
+def test_softmax_grad_bf16(N, V, stride, off):
     """bf16(-g_n softmax(x_n)) of vocabulary-major logits: within 2^-8 of the
     fp64 value (plus the fp32 evaluation's ~3e-6 relative), zeros for a
-    token with g == 0, any row stride and token tail."""
+    token with g == 0, any row stride, token and vocabulary tails, and
+    logits that do not start on a 16-byte boundary (off = 1)."""
     g0 = torch.Generator(device="cuda:0").manual_seed(N + V)
     big = torch.randn(V, stride, generator=g0, device="cuda:0") * 3.0
-    xt = big[:, :N]                     # [V, N], token n's logits are column n
+    xt = big[:, off:off + N]            # [V, N], token n's logits are column n
     xt[9, min(4, N - 1)] = 50.0         # p ~ 1 at one token
     g = torch.randn(N, generator=g0, device="cuda:0")
     g[min(2, N - 1)] = 0.0
