@@ -83,7 +83,8 @@ __device__ __forceinline__ float rank_key_y(uint64_t k) { return unord32((uint32
 // x / T rounded to nearest even, the IEEE quotient, for 2^-20 <= T <= 1024,
 // with rT = RN(1 / T) and bh = RN(T 2^-25 (1 - 2^-20)) set once per call.
 // q0 = RN(x rT) lies within 2 ulp of x / T; one correction with its fma
-// residual, q = fma(x - q0 T, rT, q0), is almost always the rounded quotient.
+// residual, q = fma(x - q0 T, rT, q0) (Markstein's correction step), is
+// almost always the rounded quotient.
 // The check is exact whatever q is: with q = f 2^e (f in [0.5, 1)) and
 // r = RN(x - q T) (one fma), |r| < bh 2^e gives |x - q T| < T ulp(q) / 2
 // (r's own rounding is inside the 2^-20 margin, and with |q| >= 2^-60 it
