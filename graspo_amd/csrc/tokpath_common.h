@@ -98,8 +98,9 @@ __device__ __forceinline__ float div_by_t(float x, float T, float rT, float bh) 
   const float q = __builtin_fmaf(__builtin_fmaf(-q0, T, x), rT, q0);
   const float r = __builtin_fmaf(-q, T, x);
   const int e = __builtin_amdgcn_frexp_expf(q);
-  const bool ok = (__builtin_fabsf(r) < __builtin_ldexpf(bh, e)) & (e >= -59) &
-                  ((f2u(q) & 0x7FFFFFu) != 0u);
+  // (bitwise: all three tests are evaluated, no branch between them)
+  const bool ok = ((int)(__builtin_fabsf(r) < __builtin_ldexpf(bh, e)) & (int)(e >= -59) &
+                   (int)((f2u(q) & 0x7FFFFFu) != 0u)) != 0;
   if (__builtin_expect(ok, 1)) return q;
   // (the empty asm keeps the division in its own block, off the common path)
   asm volatile("" ::: "memory");

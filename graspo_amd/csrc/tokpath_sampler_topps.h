@@ -84,7 +84,6 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
   const int64_t s1 = s0 + vps < nvec ? s0 + vps : nvec;
   const uint32_t nch = (uint32_t)((s1 - s0 + kChunk - 1) / kChunk);
   const bool ragged = ((s1 - s0) % kChunk) != 0;  // the slice's last chunk is partial
-  auto rot = [&](int j) -> int { return (j + (tid >> 2)) & (kPer - 1); };
 
   // ---- 0. the first two chunks of each wave in flight, then the clear
   const uint32_t last_word = (uint32_t)((V - 1) >> 5);
