@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from graspo_amd import workloads as W
+from graspo_amd import ops, workloads as W
 from tests._util import oracle_sample
 from tests.test_gpu_sampler import assert_parity, gpu_sample
 
@@ -195,3 +195,25 @@ def test_fuzz_large_vocab():
                                           dtype=torch.int32)
             kw["repetition_penalty"] = float(rng.choice([0.7, 1.05, 1.3, 2.0]))
         _check(x, f"fuzz {case}", **kw)
+
+
+@pytest.mark.parametrize("T", [0.7, 0.3, 1.7])
+def test_quotients_near_rounding_midpoints(T):
+    """Every logit is chosen so that x / T lies within a few ulp of the
+    midpoint between two fp32 values (y0 + ulp / 2, then x nudged by -1, 0 or
+    +1 ulp): the kernel's division by T, a corrected reciprocal product
+    accepted only when provably the IEEE quotient, must give the oracle's y
+    bit for bit, which the threshold value output shows."""
+    B, V = 16, 65536 + 5
+    rng = np.random.default_rng(int(T * 1000))
+    y0 = (rng.standard_normal((B, V)) * 4.0).astype(np.float32)
+    y0[y0 == 0] = np.float32(1.0)
+    mid = y0.astype(np.float64) + np.sign(y0) * np.spacing(np.abs(y0)).astype(np.float64) / 2
+    x = (mid * np.float64(np.float32(T))).astype(np.float32)
+    step = rng.integers(-1, 2, size=x.shape)
+    x = np.where(step > 0, np.nextafter(x, np.float32(np.inf)),
+                 np.where(step < 0, np.nextafter(x, np.float32(-np.inf)), x)).astype(np.float32)
+    g = torch.Generator().manual_seed(5)
+    xg = aligned_rows(torch.from_numpy(x))
+    assert ops.sample_route(xg, temperature=T, top_p=0.9)[0] == ops.ROUTE_TOPP32
+    _check(xg, f"midpoints T {T}", temperature=T, top_p=0.9, uniforms=_u(B, g))
