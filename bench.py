@@ -43,8 +43,7 @@ expression, with the bf16 GEMM's TFLOP/s against the matrix-core peak.
 top-p only -- the decode loop's T 0.7 / P 0.9 rows, and the same with the
 history and mask -- on the top-p kernel), each call timed alone (a
 read-only pass over a 512 MB buffer evicts the MALL and the GPU drains
-before every launch; a top-p call's time spans its kernel and the hand-over
-kernel), and the loss-side
+before every launch; every call is one kernel launch), and the loss-side
 logprob workload: bf16 [32768,151936] x 2 passes (policy and reference
 logits) in 4 chunks of 8192 rows each.
 

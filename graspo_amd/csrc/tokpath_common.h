@@ -294,11 +294,10 @@ __device__ __forceinline__ void load_group(const T* row, int64_t G, int64_t V, b
 // Events that the next launch through launch_timed records at its start and
 // end (hipExtLaunchKernelGGL takes them from the dispatch itself), set by
 // gtp_time_next_launch; per host thread, cleared by the launch that uses them.
-// A call of two launches (a top-p kernel and its hand-over kernel) starts the
-// first with launch_timed_head, which records only `start` and keeps `stop`
-// for the launch_timed_tail that follows, so the pair brackets the call.
+// Every call times as one launch: the top-p kernels run the row-wise path for
+// the rows they cannot take inside the same launch.
 struct LaunchEvents {
-  hipEvent_t start, stop, pending_stop;
+  hipEvent_t start, stop;
 };
 extern thread_local LaunchEvents g_next_launch_events;
 
@@ -307,29 +306,7 @@ inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, hipStream_t s, Ar
   LaunchEvents& e = g_next_launch_events;
   if (e.start && e.stop) {
     hipExtLaunchKernelGGL(kernel, grid, block, 0, s, e.start, e.stop, 0, args...);
-    e = LaunchEvents{nullptr, nullptr, nullptr};
-  } else {
-    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
-  }
-}
-
-template <typename Kernel, typename... Args>
-inline void launch_timed_head(Kernel kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
-  LaunchEvents& e = g_next_launch_events;
-  if (e.start && e.stop) {
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, e.start, nullptr, 0, args...);
-    e = LaunchEvents{nullptr, nullptr, e.stop};
-  } else {
-    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
-  }
-}
-
-template <typename Kernel, typename... Args>
-inline void launch_timed_tail(Kernel kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
-  LaunchEvents& e = g_next_launch_events;
-  if (e.pending_stop) {
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, nullptr, e.pending_stop, 0, args...);
-    e.pending_stop = nullptr;
+    e = LaunchEvents{nullptr, nullptr};
   } else {
     hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
   }

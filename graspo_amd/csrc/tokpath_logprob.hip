@@ -335,13 +335,13 @@ extern "C" int gtp_logprob_entropy_rows(const void* logits, int dtype, int64_t N
 }
 
 namespace gtp {
-thread_local LaunchEvents g_next_launch_events{nullptr, nullptr, nullptr};
+thread_local LaunchEvents g_next_launch_events{nullptr, nullptr};
 }
 
 extern "C" int gtp_time_next_launch(void* start_event, void* stop_event) {
   if (!start_event || !stop_event) return GTP_ERR_INVALID_ARGUMENT;
   g_next_launch_events = LaunchEvents{reinterpret_cast<hipEvent_t>(start_event),
-                                      reinterpret_cast<hipEvent_t>(stop_event), nullptr};
+                                      reinterpret_cast<hipEvent_t>(stop_event)};
   return GTP_OK;
 }
 

@@ -2069,43 +2069,12 @@ using namespace gtp;
 
 namespace gtp {
 
-// The rows a top-p kernel handed over (handover[0] of them, indices in
-// handover[2..]), on the row-wise path: workgroup i of a grid of B takes the
-// i-th listed row.  Every workgroup reads what it needs, then arrives at the
-// counter handover[1]; the last one returns the count, the counter and the
-// list to zero, so the workspace is all zero again for the next call (the
-// split kernel's arrival counters share its first 64 words, which every
-// kernel leaves zero).  With no row handed over each workgroup reads one word
-// and exits.
-template <typename T>
-__global__ __launch_bounds__(kSB) void sampler_handover_kernel(SamplerArgs a,
-                                                               uint32_t* __restrict__ handover) {
-  __shared__ SamplerSmem sm;
-  __shared__ uint32_t last;
-  const uint32_t n = handover[0];
-  if (n == 0u) return;
-  const uint32_t i = blockIdx.x;
-  if (i < n) rowwise_row<T>(a, (int64_t)handover[2 + i], sm);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    last = atomicAdd(&handover[1], 1u) == gridDim.x - 1u ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (uint32_t j = threadIdx.x; j < n + 2u; j += kSB) handover[j] = 0u;
-}
-
 // Top-p rows without top-k that the top-p kernels take (bf16 or fp32).
 bool topp_takes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p) {
   const bool top_p = p->top_p > 0.0f && p->top_p < 1.0f && (p->top_k <= 0 || (int64_t)p->top_k >= V);
   return (dtype == GTP_DTYPE_BF16 || dtype == GTP_DTYPE_F32) && p->temperature > 0.0f &&
          p->temperature <= 1024.0f && top_p && V >= topp::kMinV && V <= GTP_SAMPLER_MAX_V && B > 0;
 }
-
-// the hand-over count, arrival counter and list
-size_t topp_list_bytes(int64_t B) { return ((size_t)(B + 2) * 4 + 255) / 256 * 256; }
 
 ToppSplit plan_topp_split(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap) {
   ToppSplit pl{0, 0, 0};
@@ -2132,22 +2101,21 @@ ToppSplit plan_topp_split(int dtype, int64_t B, int64_t V, const gtp_sampler_par
 size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap) {
   if (!topp_takes(dtype, B, V, p)) return 0;
   const ToppSplit sp = plan_topp_split(dtype, B, V, p, cap);
-  return sp.S ? sp.bytes : topp_list_bytes(B);
+  return sp.S ? sp.bytes : 0;
 }
 
 GeneralRoute route_general(int dtype, int64_t B, int64_t V, bool aligned, int64_t hist_len,
                            bool has_mask, const gtp_sampler_params* p, bool has_ws,
                            size_t workspace_bytes) {
   GeneralRoute r{GTP_ROUTE_ROWWISE, ToppSplit{0, 0, 0}};
-  // top-p rows without top-k: the single-read top-p kernels, then the
-  // row-wise path for any row they hand over (the hand-over list lives in the
-  // workspace; without one, the value-histogram kernel takes the call)
-  const size_t tw = topp_takes(dtype, B, V, p) ? topp_list_bytes(B) : 0;
+  // top-p rows without top-k: the top-p kernels (each runs the row-wise path
+  // itself for a row outside its bounds)
+  const bool tp = topp_takes(dtype, B, V, p);
   const bool pen = hist_len > 0 && p->repetition_penalty != 1.0f;
   // (penalised counts are 16-bit: at most 65535 history entries)
   // (rows with a mask and no penalty: the split kernel gains nothing from
   // 32 rows on, [64, 151936] 43.4 against 42.1 us)
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535 && has_ws &&
+  if (tp && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535 && has_ws &&
       (pen || !has_mask || B <= 32)) {
     // few bf16 rows: each row split over S workgroups (the workspace holds
     // their counters, headers and slots)
@@ -2158,12 +2126,11 @@ GeneralRoute route_general(int dtype, int64_t B, int64_t V, bool aligned, int64_
       return r;
     }
   }
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_F32 && has_ws && workspace_bytes >= tw) {
+  if (tp && aligned && dtype == GTP_DTYPE_F32) {
     r.route = GTP_ROUTE_TOPP32;  // two reads, the candidates of the cut in LDS
     return r;
   }
-  if (tw > 0 && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535 && has_ws &&
-      workspace_bytes >= tw) {
+  if (tp && aligned && dtype == GTP_DTYPE_BF16 && hist_len <= 65535) {
     r.route = GTP_ROUTE_TOPP;
     return r;
   }
@@ -2190,37 +2157,33 @@ int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream
   const GeneralRoute r = route_general(dtype, B, a.V, aligned, a.hist ? a.hist_len : 0,
                                        a.mask != nullptr, &p, workspace != nullptr,
                                        workspace_bytes);
-  uint32_t* handover = reinterpret_cast<uint32_t*>(workspace);
   switch (r.route) {
     case GTP_ROUTE_TOPP_SPLIT: {
       unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
       const dim3 sgrid((unsigned)r.split.S, (unsigned)B);
       switch (mode) {
-        case 0: launch_timed_head(sampler_topps_kernel<0>, sgrid, block, s, a, ws, r.split.vps); break;
-        case 1: launch_timed_head(sampler_topps_kernel<1>, sgrid, block, s, a, ws, r.split.vps); break;
-        case 2: launch_timed_head(sampler_topps_kernel<2>, sgrid, block, s, a, ws, r.split.vps); break;
-        default: launch_timed_head(sampler_topps_kernel<3>, sgrid, block, s, a, ws, r.split.vps); break;
+        case 0: launch_timed(sampler_topps_kernel<0>, sgrid, block, s, a, ws, r.split.vps); break;
+        case 1: launch_timed(sampler_topps_kernel<1>, sgrid, block, s, a, ws, r.split.vps); break;
+        case 2: launch_timed(sampler_topps_kernel<2>, sgrid, block, s, a, ws, r.split.vps); break;
+        default: launch_timed(sampler_topps_kernel<3>, sgrid, block, s, a, ws, r.split.vps); break;
       }
-      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
       break;
     }
     case GTP_ROUTE_TOPP32:
       switch (mode) {
-        case 0: launch_timed_head(sampler_topp32_kernel<0>, grid, block, s, a, handover); break;
-        case 1: launch_timed_head(sampler_topp32_kernel<1>, grid, block, s, a, handover); break;
-        case 2: launch_timed_head(sampler_topp32_kernel<2>, grid, block, s, a, handover); break;
-        default: launch_timed_head(sampler_topp32_kernel<3>, grid, block, s, a, handover); break;
+        case 0: launch_timed(sampler_topp32_kernel<0>, grid, block, s, a); break;
+        case 1: launch_timed(sampler_topp32_kernel<1>, grid, block, s, a); break;
+        case 2: launch_timed(sampler_topp32_kernel<2>, grid, block, s, a); break;
+        default: launch_timed(sampler_topp32_kernel<3>, grid, block, s, a); break;
       }
-      launch_timed_tail(sampler_handover_kernel<float>, grid, block, s, a, handover);
       break;
     case GTP_ROUTE_TOPP:
       switch (mode) {
-        case 0: launch_timed_head(sampler_topp_kernel<0>, grid, block, s, a, handover); break;
-        case 1: launch_timed_head(sampler_topp_kernel<1>, grid, block, s, a, handover); break;
-        case 2: launch_timed_head(sampler_topp_kernel<2>, grid, block, s, a, handover); break;
-        default: launch_timed_head(sampler_topp_kernel<3>, grid, block, s, a, handover); break;
+        case 0: launch_timed(sampler_topp_kernel<0>, grid, block, s, a); break;
+        case 1: launch_timed(sampler_topp_kernel<1>, grid, block, s, a); break;
+        case 2: launch_timed(sampler_topp_kernel<2>, grid, block, s, a); break;
+        default: launch_timed(sampler_topp_kernel<3>, grid, block, s, a); break;
       }
-      launch_timed_tail(sampler_handover_kernel<uint16_t>, grid, block, s, a, handover);
       break;
     case GTP_ROUTE_HIST:
       if (a.mask)

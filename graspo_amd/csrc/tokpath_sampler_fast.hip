@@ -1575,8 +1575,8 @@ int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_
   if (!pl.fast) {
     const size_t tw = topp_workspace_bytes(dtype, B, V, params, workspace_bytes);
     if (clear_counters && tw > 0 && workspace && workspace_bytes >= tw) {
-      // the hand-over count and counter; with a split, the whole zero region
-      const int64_t nw = tw >= kWsZeroBytes ? (int64_t)(kWsZeroBytes / 4) : 2;
+      // the split top-p kernel's zero region (its per-row arrival counters)
+      const int64_t nw = (int64_t)(kWsZeroBytes / 4);
       hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st,
                          reinterpret_cast<uint32_t*>(workspace), nw);
     }

@@ -32,17 +32,16 @@ struct SamplerArgs {
   int32_t* out_status;
 };
 
-// One workgroup of 1024 threads per row (any layout, V <= GTP_SAMPLER_MAX_V).
-// Top-p bf16 rows use `workspace` (topp_workspace_bytes of it, zeroed once)
-// for the rows the top-p kernel hands over to the row-wise path.
+// One workgroup of 1024 threads per row (any layout, V <= GTP_SAMPLER_MAX_V),
+// or, for small batches of bf16 top-p rows, S workgroups per row that merge
+// their counts through `workspace` (topp_workspace_bytes of it, zeroed once).
 int launch_sampler_general(const SamplerArgs& a, int dtype, int64_t B, hipStream_t s,
                            void* workspace, size_t workspace_bytes);
 
 
 // The first kWsZeroBytes of a sampler workspace are words that every call
-// leaves zero: the top-p kernels' hand-over count, arrival counter and list
-// (words 0, 1, 2..), the split kernel's per-row arrival counters (words
-// 0..B-1, B < CUs) and the split top-p kernel's (word kToppSplitCtrWord + b).
+// leaves zero: the split kernel's per-row arrival counters (words 0..B-1,
+// B < CUs) and the split top-p kernel's (word kToppSplitCtrWord + b).
 // The kernels' slot data lies after it, so a call never finds another call's
 // slot data in its counters.
 constexpr size_t kWsZeroBytes = 16384;
@@ -77,9 +76,9 @@ GeneralRoute route_general(int dtype, int64_t B, int64_t V, bool aligned, int64_
                            bool has_mask, const gtp_sampler_params* p, bool has_ws,
                            size_t workspace_bytes);
 
-// Workspace of the top-p path for these parameters within `cap` bytes (0
-// when another path takes the call): the split kernel's counters, headers
-// and slots, or the hand-over count and list of rows.
+// Workspace of the top-p path for these parameters within `cap` bytes: the
+// split top-p kernel's counters, headers and slots (0 when the call takes
+// another path, the one-workgroup top-p kernels included).
 size_t topp_workspace_bytes(int dtype, int64_t B, int64_t V, const gtp_sampler_params* p, size_t cap);
 
 // Greedy decoding (T <= 0) is the reference's logits.argmax(dim=-1)

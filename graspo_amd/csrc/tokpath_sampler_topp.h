@@ -41,9 +41,9 @@
 //    it; otherwise from one more read of the row.
 // Outside these bounds (an escape, a 16-bit count overflow, a penalised
 // value above every bin, more than 48 penalised values in one resolved
-// range) the row is handed over to the row-wise path, which runs in a
-// second launch; the decision is block-uniform and taken before any output
-// of the row is written.
+// range) the row is handed over to the row-wise path, which the same
+// workgroup runs in the same launch; the decision is block-uniform and taken
+// before any output of the row is written.
 #pragma once
 
 namespace gtp {
@@ -1320,19 +1320,24 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
 
 }  // namespace topp
 
-// One row per workgroup.  A row outside the top-p path's bounds is handed
-// over: its index goes to handover[2 + n] with n = handover[0]++, and
-// sampler_handover_kernel, launched right after on the same stream, runs the
-// row-wise path for the listed rows and returns the list to zero.  The
-// row-wise path's registers thus never weigh on this kernel.
+// One row per workgroup.  A row outside the top-p path's bounds (topp_row
+// returns false, the same in every thread, before any output is written)
+// runs the row-wise path in the same workgroup, in the same LDS: a top-p
+// call is one launch.  The row-wise path raises the kernel to 128 VGPRs and
+// 240 bytes of scratch per lane (its own spills), which costs less than a
+// second launch did.
 // kMode bit 0: repetition penalty active; bit 1: allow mask.
 template <int kMode>
-__global__ __launch_bounds__(topp::kB) void sampler_topp_kernel(SamplerArgs a,
-                                                                uint32_t* __restrict__ handover) {
-  __shared__ topp::Smem sm;
+__global__ __launch_bounds__(topp::kB) void sampler_topp_kernel(SamplerArgs a) {
+  __shared__ union {
+    topp::Smem t;
+    SamplerSmem g;
+  } smu;
   const int64_t b = blockIdx.x;
-  if (!topp::topp_row<kMode>(a, b, sm) && threadIdx.x == 0)
-    handover[2 + atomicAdd(handover, 1u)] = (uint32_t)b;
+  if (!topp::topp_row<kMode>(a, b, smu.t)) {
+    __syncthreads();  // every thread is done with the top-p state
+    rowwise_row<uint16_t>(a, b, smu.g);
+  }
 }
 
 }  // namespace gtp

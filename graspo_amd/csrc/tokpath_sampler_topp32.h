@@ -849,17 +849,22 @@ __device__ __forceinline__ bool topp32_row(const SamplerArgs& a, int64_t b, Smem
 
 }  // namespace tp32
 
-// One row per workgroup; a row outside the fp32 top-p path's bounds goes to
-// the hand-over list (handover[2 + n], n = handover[0]++) for the row-wise
-// path, launched right after on the same stream.
+// One row per workgroup; a row outside the fp32 top-p path's bounds
+// (topp32_row returns false, the same in every thread, before any output is
+// written) runs the row-wise path in the same workgroup and LDS, so the call
+// is one launch.
 // kMode bit 0: repetition penalty active; bit 1: allow mask.
 template <int kMode>
-__global__ __launch_bounds__(tp32::kB) void sampler_topp32_kernel(SamplerArgs a,
-                                                                  uint32_t* __restrict__ handover) {
-  __shared__ tp32::Smem sm;
+__global__ __launch_bounds__(tp32::kB) void sampler_topp32_kernel(SamplerArgs a) {
+  __shared__ union {
+    tp32::Smem t;
+    SamplerSmem g;
+  } smu;
   const int64_t b = blockIdx.x;
-  if (!tp32::topp32_row<kMode>(a, b, sm) && threadIdx.x == 0)
-    handover[2 + atomicAdd(handover, 1u)] = (uint32_t)b;
+  if (!tp32::topp32_row<kMode>(a, b, smu.t)) {
+    __syncthreads();  // every thread is done with the top-p state
+    rowwise_row<float>(a, b, smu.g);
+  }
 }
 
 }  // namespace gtp

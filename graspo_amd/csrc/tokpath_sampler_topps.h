@@ -24,9 +24,8 @@
 // 3. Ids.  The slots' counts of the cut's and the draw's values say which
 //    slice holds each wanted token and its rank among the value's tokens
 //    there; one more read of that slice (or of both) finds them.
-// A row outside the bounds is handed over (its index to the hand-over list,
-// for sampler_handover_kernel, launched right after), as in the
-// one-workgroup kernel.
+// A row outside the bounds runs the row-wise path in its last workgroup, as
+// in the one-workgroup kernel.
 #pragma once
 
 // The publication of slice counts below relies on gfx950's code generation
@@ -46,8 +45,8 @@ constexpr int kMaxS = 8;            // slices per row
 constexpr int kHdrWords = 16;
 constexpr int kSlotWords = kHistWords;  // a slot mirrors the bins' word layout
 
-// Workspace of a split call: the zero region (hand-over words, the per-row
-// arrival counters at word kToppSplitCtrWord), the headers, the slots.
+// Workspace of a split call: the zero region (the per-row arrival counters
+// at word kToppSplitCtrWord), the headers, the slots.
 __device__ __forceinline__ uint32_t* split_headers(unsigned char* ws) {
   return reinterpret_cast<uint32_t*>(ws + kWsZeroBytes);
 }
@@ -648,20 +647,26 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
 }  // namespace topps
 
 // Workgroup (s, b) takes slice s of row b; the row's last workgroup to
-// arrive finishes it.  A row outside the top-p path's bounds goes to the
-// hand-over list (handover[2 + n], n = handover[0]++) for
-// sampler_handover_kernel, launched right after on the same stream.
+// arrive finishes it.  A row outside the top-p path's bounds (only the last
+// workgroup decides, the same in all its threads, before any output is
+// written) runs the row-wise path in that workgroup and LDS, so the call is
+// one launch.
 // kMode bit 0: repetition penalty active; bit 1: allow mask.
 template <int kMode>
 __global__ __launch_bounds__(topp::kB) void sampler_topps_kernel(SamplerArgs a, unsigned char* __restrict__ ws,
                                                                  int64_t vps) {
-  __shared__ topp::Smem sm;
-  __shared__ topps::Extra ex;
+  __shared__ union {
+    struct {
+      topp::Smem sm;
+      topps::Extra ex;
+    } t;
+    SamplerSmem g;
+  } smu;
   const int64_t b = blockIdx.y;
-  if (!topps::topps_row<kMode>(a, b, (int)blockIdx.x, (int)gridDim.x, vps, (int64_t)gridDim.y, ws, sm, ex) &&
-      threadIdx.x == 0) {
-    uint32_t* handover = reinterpret_cast<uint32_t*>(ws);
-    handover[2 + atomicAdd(handover, 1u)] = (uint32_t)b;
+  if (!topps::topps_row<kMode>(a, b, (int)blockIdx.x, (int)gridDim.x, vps, (int64_t)gridDim.y, ws, smu.t.sm,
+                               smu.t.ex)) {
+    __syncthreads();  // every thread is done with the top-p state
+    rowwise_row<uint16_t>(a, b, smu.g);
   }
 }
 

@@ -149,13 +149,11 @@ int gtp_sample_rows(const void* logits, int dtype, int64_t B, int64_t V,
  * gtp_sample_workspace_bytes -- workspace gtp_sample_rows needs for B rows of
  * V logits of `dtype` under `params` (0 when the call needs none).  Greedy and
  * top-k rows (1 <= top_k <= 128) split each row over several workgroups and
- * merge per-row candidate lists through the workspace.  Top-p rows without
- * top-k at V >= 65536 (bf16, fp32) keep a hand-over list there, and bf16
- * top-p batches of up to 64 rows also split each row over several
+ * merge per-row candidate lists through the workspace.  bf16 top-p batches
+ * (no top-k, V >= 65536) of up to 64 rows also split each row over several
  * workgroups, which merge their value counts through 64 KB slots (16.8 MB
- * for 64 rows of 151936).  A smaller workspace, at least the hand-over
- * list's (B + 2) * 4 bytes rounded up to 256, gives those top-p calls fewer
- * slices or one workgroup per row; other calls need none.
+ * for 64 rows of 151936); a smaller workspace gives them fewer slices, and
+ * none one workgroup per row.  Other calls need none.
  */
 size_t gtp_sample_workspace_bytes(int dtype, int64_t B, int64_t V,
                                   const gtp_sampler_params* params);
@@ -454,10 +452,10 @@ int gtp_f32_to_bf16_exact(const float* src, int64_t n, uint16_t* dst,
  * gtp_time_next_launch -- measurement hook, no counterpart in the reference:
  * the next gtp_sample_rows, gtp_logprob_entropy_rows, gtp_logprob_backward_rows
  * or gtp_stream_read_rows call from the calling thread records start_event
- * when its first kernel's dispatch begins and stop_event when its last
- * kernel ends (hipExtLaunchKernelGGL; a top-p sampler call launches its
- * kernel and the hand-over kernel), so the two HIP events bracket the call's
- * kernels, without the idle time of event packets recorded around them.
+ * when its kernel's dispatch begins and stop_event when it ends
+ * (hipExtLaunchKernelGGL; each of these calls is one launch), so the two HIP
+ * events bracket the call's kernel, without the idle time of event packets
+ * recorded around it.
  * Both are hipEvent_t created by the caller (with timing).  The hook is per
  * thread and used once; the benchmark is its caller.
  */

@@ -108,14 +108,14 @@ def sample_args(logits: torch.Tensor, *, temperature, top_k=0, top_p=1.0,
 
 
 def sample_small_workspace(logits: torch.Tensor, **kw):
-    """gtp_sample_rows with a fresh zeroed workspace of only the top-p
-    hand-over list's bytes (B + 2 words): a top-p call then takes the
-    one-workgroup top-p kernel whatever B is.  Returns the outputs on the
-    CPU as a dict of the SampleOutput fields."""
+    """gtp_sample_rows with a fresh zeroed workspace of 256 bytes, too small
+    for the split top-p kernel: a top-p call then takes the one-workgroup
+    top-p kernel whatever B is.  Returns the outputs on the CPU as a dict of
+    the SampleOutput fields."""
     L = lib()
     dev = logits.device
     args, p, B = sample_args(logits, **kw)
-    nbytes = ((B + 2) * 4 + 255) // 256 * 256
+    nbytes = 256
     ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
     out = SampleBuffers(B, dev)
     rc = L.gtp_sample_rows(*args, *out.out_args(), ws.data_ptr(), nbytes, stream_handle())

@@ -64,19 +64,24 @@ int main(void) {
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 4, 0, &topp), 0);
   EXPECT_RC(w, (int)(gtp_sample_workspace_bytes(1, INT64_MAX, 151936, &topp) != 0), 0);
   EXPECT_RC(w, (int)(gtp_sample_workspace_bytes(1, 64, INT64_MAX, &topp) != 0), 0);
-  /* top-p rows of a large batch (and fp32 rows): the hand-over count and
-     list, rounded to 256 bytes */
-  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 256, 151936, &topp), 1280);
-  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(0, 64, 151936, &topp), 512);
+  /* top-p rows of a large batch (and fp32 rows): one workgroup per row, no
+     workspace */
+  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 256, 151936, &topp), 0);
+  EXPECT_RC(w, (int)gtp_sample_workspace_bytes(0, 64, 151936, &topp), 0);
   /* bf16 top-p rows of a small batch, split over S = 4 workgroups per row
      (no device here: 256 CUs assumed): 16 KB of counters, 64 x 4 headers of
      64 bytes, 64 x 4 slots of 64 KB */
   EXPECT_RC(w, (int)gtp_sample_workspace_bytes(1, 64, 151936, &topp), 16384 + 16384 + 64 * 4 * 65536);
-  /* the library's own workspace is bounded */
-  EXPECT_RC(w, gtp_sample_rows_noalloc(L, 1, (int64_t)1 << 30, 151936, 151936, NULL, 0, 0, NULL,
-                                       0, F, &topp, NULL, 0, PH(int64_t*), NULL, NULL, NULL, NULL,
-                                       NULL, NULL, NULL),
-            X);
+  /* the library's own workspace is bounded: 8192 fp32 rows of 2^18 with
+     top-k 128 merge more candidate lists than it holds */
+  {
+    const gtp_sampler_params topk = {1.0f, 128, 1.0f, 1.0f};
+    EXPECT_RC(w, (int)(gtp_sample_workspace_bytes(0, 8192, 1 << 18, &topk) > GTP_NOALLOC_SCRATCH_BYTES), 1);
+    EXPECT_RC(w, gtp_sample_rows_noalloc(L, 0, 8192, 1 << 18, 1 << 18, NULL, 0, 0, NULL, 0, F, &topk,
+                                         NULL, 0, PH(int64_t*), NULL, NULL, NULL, NULL, NULL, NULL,
+                                         NULL),
+              X);
+  }
 
   EXPECT_RC(w, gtp_lse_partial_rows(L, 1, -1, 10, 10, 0, T, 0, o, 0, NULL), I);
   EXPECT_RC(w, gtp_lse_partial_rows(L, 1, 4, 0, 10, 0, T, 0, o, 0, NULL), I);

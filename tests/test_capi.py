@@ -55,9 +55,11 @@ def test_sample_route_on_the_host():
     assert R.route(L, BF16, 64, 151936, T=0.8, P=0.9, mask=True) == (R.ROUTE_TOPP, 1)
     assert R.route(L, BF16, 256, 248320, T=0.7, P=0.9) == (R.ROUTE_TOPP, 1)
     assert R.route(L, F32, 256, 248320, T=0.7, P=0.9) == (R.ROUTE_TOPP32, 1)
-    # without a workspace the top-p kernels (hand-over list) are out
-    assert R.route(L, F32, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_ROWWISE, 1)
-    assert R.route(L, BF16, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_HIST, 1)
+    # the one-workgroup top-p kernels need no workspace; the split one does
+    assert R.route(L, F32, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_TOPP32, 1)
+    assert R.route(L, BF16, 256, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_TOPP, 1)
+    assert R.route(L, BF16, 16, 248320, T=0.7, P=0.9, workspace=0) == (R.ROUTE_TOPP, 1)
+    assert R.route(L, BF16, 4, 70000, T=1.0, P=0.9, workspace=0, aligned=False)[0] == R.ROUTE_ROWWISE
     # the allocation-free entry point's 8 MiB array: 7 slices for 16 decode rows
     assert R.route(L, BF16, 16, 248320, T=0.7, P=0.9)[0] == R.ROUTE_TOPP_SPLIT
     assert R.route(L, BF16, 16, 248320, T=0.7, P=0.9,

@@ -66,10 +66,10 @@ def test_hook_needs_existing_events():
                              torch.cuda.Event(enable_timing=True))
 
 
-def test_hook_brackets_both_launches_of_a_top_p_call():
-    """A top-p call launches its kernel and the hand-over kernel: the events
-    span both, so a row handed over to the row-wise path (a -inf logit is
-    outside the top-p kernel's bins) adds its time to the hooked interval."""
+def test_hook_spans_a_row_that_takes_the_row_wise_path():
+    """A top-p call is one launch: a row outside the top-p kernel's bounds (a
+    -inf logit is outside its bins) runs the row-wise path in the same
+    kernel, so its time shows in the hooked interval."""
     g = torch.Generator(device=DEV).manual_seed(5)
     x = (torch.randn(128, 151936, device=DEV, generator=g) * 2.0).to(torch.bfloat16)
     u = ops.draw_uniforms(128, DEV, g)

@@ -38,9 +38,8 @@ def _u(B, g):
 
 
 def one_workgroup_sample(x, **kw):
-    """The call through the C ABI with a workspace that holds only the
-    hand-over list, so that rows of a small batch take the one-workgroup
-    kernel instead of the split one."""
+    """The call through the C ABI with a workspace too small for the split
+    kernel, so that rows of a small batch take the one-workgroup kernel."""
     dev = torch.device("cuda:0")
     kw = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
     if kw.get("finished") is not None:
@@ -209,9 +208,9 @@ def test_status_rows_and_padding():
 
 
 def test_workspace_shared_with_the_split_kernel():
-    """The torch glue keeps one workspace per stream for the split kernel's
-    arrival counters and the top-p hand-over list: alternate the two kinds
-    of call (with rows handed over) and check every call."""
+    """The torch glue keeps one workspace per stream for the arrival counters
+    of the split top-k and split top-p kernels: alternate the two kinds of
+    call (with rows that go to the row-wise path) and check every call."""
     g = torch.Generator().manual_seed(14)
     B, V = 64, 151936
     x = (torch.randn(B, V, generator=g) * 2.5).to(torch.bfloat16)
