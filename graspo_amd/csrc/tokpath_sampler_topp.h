@@ -234,7 +234,7 @@ __device__ __forceinline__ void weight_scan(Smem& sm, unsigned long long Wt, uin
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const unsigned long long iw = wave_scan_u64(Wt);
   const uint32_t ic = wave_scan_u32(Nt);
-  const uint32_t s2 = wave_sum_u32(n2);
+  const uint32_t s2 = wave_total_u32(n2);
   if (kMode == 2) wave_lse2(lm, lsum);
   else if (kMode != 3) lsum = wave_sum_f(lsum);
   __syncthreads();  // (own is read)
@@ -253,7 +253,7 @@ __device__ __forceinline__ void weight_scan(Smem& sm, unsigned long long Wt, uin
     const float fm = in ? sm.red_f[lane][0] : kNegInf, fs = in ? sm.red_f[lane][1] : 0.0f;
     const unsigned long long pw = wave_scan_u64(vw);
     const uint32_t pc = wave_scan_u32(vc);
-    const uint32_t t2 = wave_sum_u32(v2);
+    const uint32_t t2 = wave_total_u32(v2);
     const float mm = wave_max_f(fm);
     float ss = 0.0f;
     if (kMode == 2) ss = wave_sum_f(fs > 0.0f ? fs * __builtin_amdgcn_exp2f((fm - mm) * kLog2e) : 0.0f);
@@ -446,7 +446,7 @@ __device__ __forceinline__ bool resolve(const Smem& sm, const Row& r, float m, u
   const uint32_t ic_b = gs ? (uint32_t)__builtin_amdgcn_readlane((int)ic, gs - 1) : 0u;
   const bool in_grp = (grp >> lane) & 1ull;
   // the group's members (at most one unpenalised and one penalised value)
-  const uint32_t gn = wave_sum_u32(in_grp ? cs : 0u);
+  const uint32_t gn = wave_total_u32(in_grp ? cs : 0u);
   const unsigned long long bu = __ballot(in_grp && kinds == 0);
   const unsigned long long bp = __ballot(in_grp && kinds == 1);
   const int ub = bu ? __builtin_amdgcn_readlane(refs, __builtin_ctzll(bu)) : -1;
@@ -1016,17 +1016,12 @@ __device__ __forceinline__ bool topp_row(const SamplerArgs& a, int64_t b, Smem& 
     key = (rmax & 0xFFFFu) > (rmax >> 16) ? (rmax & 0xFFFFu) : (rmax >> 16);
   }
   Lse3 rl{kNegInf, 0.0f, 0.0f};
-  if (kMode == 3) rl = block_lse3<kB>(st, sm.red_f);
+  if (kMode == 3) rl = block_lse3_dpp<kB>(st, sm.red_f);
   {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const int oa = __shfl_xor(topA, o, kWave), ob = __shfl_xor(topB, o, kWave);
-      const uint32_t ok = (uint32_t)__shfl_xor((int)key, o, kWave);
-      topA = oa < topA ? oa : topA;
-      topB = ob < topB ? ob : topB;
-      key = ok > key ? ok : key;
-    }
-    tot = wave_sum_u32(tot);
+    topA = (int)wave_min_u32((uint32_t)topA);  // (bins are >= 0)
+    topB = (int)wave_min_u32((uint32_t)topB);
+    key = wave_max_u32(key);
+    tot = wave_total_u32(tot);
     __syncthreads();
     if (lane == 0) {
       sm.red_u[wid][0] = (uint32_t)topA;

@@ -230,7 +230,7 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
     if (kMode == 3) lse_fold_block_max<false, 1, 8>(st, xt, vec_max<8>(xt[0]));
   }
   Lse3 rl{kNegInf, 0.0f, 0.0f};
-  if (kMode == 3) rl = block_lse3<kB>(st, sm.red_f);  // (its barrier ends the stream)
+  if (kMode == 3) rl = block_lse3_dpp<kB>(st, sm.red_f);  // (its barrier ends the stream)
   else __syncthreads();
 
   // ---- 3. publish: the nonempty word range of each region (words 0..kNI
@@ -269,17 +269,11 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
         }
       }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint32_t ol = (uint32_t)__shfl_xor((int)lo, o, kWave);
-      const uint32_t oh = (uint32_t)__shfl_xor((int)hi, o, kWave);
-      const int op = __shfl_xor(pmax, o, kWave), on = __shfl_xor(nmin, o, kWave);
-      lo = ol < lo ? ol : lo;
-      hi = oh > hi ? oh : hi;
-      pmax = op > pmax ? op : pmax;
-      nmin = on < nmin ? on : nmin;
-    }
-    tot = wave_sum_u32(tot);
+    lo = wave_min_u32(lo);
+    hi = wave_max_u32(hi);
+    pmax = (int)wave_max_u32((uint32_t)(pmax + 1)) - 1;  // (pmax >= -1)
+    nmin = (int)wave_min_u32((uint32_t)nmin);            // (nmin >= 0)
+    tot = wave_total_u32(tot);
     esc = __ballot(esc != 0u) ? 1u : 0u;
     __syncthreads();  // (red_u is free)
     if (lane == 0) {
@@ -298,20 +292,25 @@ __device__ __forceinline__ bool topps_row(const SamplerArgs& a, int64_t b, int s
       const uint32_t pk = in ? sm.red_u[lane][3] : (kNI << 14);
       int pm = (int)(pk & 0x3FFFu) - 1, nm = (int)((pk >> 14) & 0x3FFFu);
       uint32_t es = pk >> 28;
-#pragma unroll
-      for (int o = 1; o < kW / 2; o <<= 1) {  // (within aligned groups of 8 lanes)
-        const uint32_t ol = (uint32_t)__shfl_xor((int)rlo, o, kWave);
-        const uint32_t oh = (uint32_t)__shfl_xor((int)rhi, o, kWave);
-        const int op = __shfl_xor(pm, o, kWave), on = __shfl_xor(nm, o, kWave);
-        nt += (uint32_t)__shfl_xor((int)nt, o, kWave);
-        es |= (uint32_t)__shfl_xor((int)es, o, kWave);
+      // within aligned groups of 8 lanes (DPP)
+      auto step = [&](auto xr) __attribute__((always_inline)) {
+        const uint32_t ol = xr(rlo), oh = xr(rhi);
+        const int op = (int)xr((uint32_t)pm), on = (int)xr((uint32_t)nm);
+        nt += xr(nt);
+        es |= xr(es);
         rlo = ol < rlo ? ol : rlo;
         rhi = oh > rhi ? oh : rhi;
         pm = op > pm ? op : pm;
         nm = on < nm ? on : nm;
-      }
-      const uint32_t nt_all = (uint32_t)__shfl((int)nt, 0, kWave) + (uint32_t)__shfl((int)nt, kW / 2, kWave);
-      const uint32_t es_all = (uint32_t)__shfl((int)es, 0, kWave) | (uint32_t)__shfl((int)es, kW / 2, kWave);
+      };
+      static_assert(kW / 2 == 8, "groups of 8 lanes");
+      step([](uint32_t v) { return lane_xor<1>(v); });
+      step([](uint32_t v) { return lane_xor<2>(v); });
+      step([](uint32_t v) { return lane_xor<4>(v); });
+      const uint32_t nt_all = (uint32_t)__builtin_amdgcn_readlane((int)nt, 0) +
+                              (uint32_t)__builtin_amdgcn_readlane((int)nt, kW / 2);
+      const uint32_t es_all = (uint32_t)__builtin_amdgcn_readlane((int)es, 0) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)es, kW / 2);
       if (lane == 0 || lane == kW / 2) {
         const int g = lane / (kW / 2);
         // smallest value bin: the largest positive value, else the negative

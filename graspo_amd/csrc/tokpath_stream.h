@@ -167,6 +167,32 @@ __device__ __forceinline__ uint32_t lane63_u32(uint32_t v) {
 __device__ __forceinline__ unsigned long long lane63_u64(unsigned long long v) {
   return ((unsigned long long)lane63_u32((uint32_t)(v >> 32)) << 32) | lane63_u32((uint32_t)v);
 }
+// Reductions over the 64 lanes, the result in every lane: the scan's DPP
+// steps (lanes without a source read the identity `id`) and a read of lane
+// 63.  Unlike __shfl_xor they keep no per-lane addresses in registers, which
+// the compiler may otherwise hoist, share with other code of the kernel and
+// spill.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_take_id(uint32_t v, uint32_t id) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, kCtrl, kRowMask, 0xF, false);
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x, uint32_t id, Op op) {
+  x = op(x, dpp_take_id<0x111, 0xF>(x, id));
+  x = op(x, dpp_take_id<0x112, 0xF>(x, id));
+  x = op(x, dpp_take_id<0x114, 0xF>(x, id));
+  x = op(x, dpp_take_id<0x118, 0xF>(x, id));
+  x = op(x, dpp_take_id<0x142, 0xA>(x, id));
+  x = op(x, dpp_take_id<0x143, 0xC>(x, id));
+  return lane63_u32(x);
+}
+__device__ __forceinline__ uint32_t wave_total_u32(uint32_t x) { return lane63_u32(wave_scan_u32(x)); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  return wave_reduce_u32(x, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return wave_reduce_u32(x, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
 // Sums within each row of 16 lanes (inclusive; lane 15 of a row holds the
 // row's total).
 __device__ __forceinline__ uint32_t row_scan_u32(uint32_t x) {
@@ -309,6 +335,37 @@ __device__ __forceinline__ Lse3 wave_lse3(Lse3 v) {
 template <int NT>
 __device__ __forceinline__ Lse3 block_lse3(Lse3 v, float (*red)[3]) {
   v = wave_lse3(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (lane == 0) {
+    red[wid][0] = v.m;
+    red[wid][1] = v.s;
+    red[wid][2] = v.t;
+  }
+  __syncthreads();
+  Lse3 r{red[0][0], red[0][1], red[0][2]};
+#pragma unroll
+  for (int w = 1; w < NT / kWave; ++w) r = lse3_merge(r, Lse3{red[w][0], red[w][1], red[w][2]});
+  return r;
+}
+// The same over the block, with the wave step on DPP and a swizzle within
+// each half of the wave and a read of lanes 0 and 32 (no per-lane shuffle
+// addresses; for kernels whose register budget is tight).
+template <int NT>
+__device__ __forceinline__ Lse3 block_lse3_dpp(Lse3 v, float (*red)[3]) {
+  auto step = [&](auto xr) __attribute__((always_inline)) {
+    v = lse3_merge(v, Lse3{u2f(xr(f2u(v.m))), u2f(xr(f2u(v.s))), u2f(xr(f2u(v.t)))});
+  };
+  step([](uint32_t x) { return lane_xor<1>(x); });
+  step([](uint32_t x) { return lane_xor<2>(x); });
+  step([](uint32_t x) { return lane_xor<4>(x); });
+  step([](uint32_t x) { return lane_xor<8>(x); });
+  step([](uint32_t x) { return lane_xor<16>(x); });
+  auto at = [&](int l) {
+    return Lse3{u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(v.m), l)),
+                u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(v.s), l)),
+                u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(v.t), l))};
+  };
+  v = lse3_merge(at(0), at(32));
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   if (lane == 0) {
     red[wid][0] = v.m;
