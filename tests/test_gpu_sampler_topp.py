@@ -168,7 +168,7 @@ def test_masked_rows():
 
 
 def test_rows_handed_over_to_the_row_wise_path():
-    """Rows outside the kernel's bounds go to the row-wise path in a second
+    """Rows outside the kernel's bounds run the row-wise path inside the same
     launch: a value beyond 2^24, a tiny nonzero value, a constant row (one
     value held by every token, beyond a 16-bit count), and a row whose
     penalised values crowd one range; the other rows of the batch stay on
@@ -185,6 +185,31 @@ def test_rows_handed_over_to_the_row_wise_path():
     hist[4] = torch.arange(4000, dtype=torch.int32)
     for kw in (dict(), dict(history=hist, repetition_penalty=1.5)):
         _check(x, f"hand-over {list(kw)}", temperature=0.8, top_p=0.9, uniforms=_u(B, g), **kw)
+
+
+@pytest.mark.parametrize("mode", ["mask", "mask + penalty"])
+def test_masked_rows_handed_over(mode):
+    """The masked variants' rows outside the kernel's bounds (an allowed -inf
+    logit, a value beyond 2^24, a constant row whose one value every allowed
+    token holds) run the row-wise path inside the same launch, in the split
+    and the one-workgroup kernels; the other rows stay on the top-p path."""
+    B, V = 8, 70000
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(B, V, generator=g) * 2
+    x[1, 500] = 3.0e7
+    x[2, 77] = float("-inf")
+    x[3] = 1.25
+    x = x.to(torch.bfloat16)
+    bits = torch.rand(B, V, generator=g) < 0.3
+    bits[1, 500] = True
+    bits[2, 77] = True
+    bits[3] = True  # 70000 allowed tokens of one value: beyond a 16-bit count
+    kw = dict(temperature=0.8, top_p=0.9, uniforms=_u(B, g), allow_mask=W.pack_mask(bits))
+    if mode == "mask + penalty":
+        hist = torch.randint(0, V, (B, 3000), generator=g, dtype=torch.int32)
+        hist[1, 0] = 500
+        kw.update(history=hist, repetition_penalty=1.3)
+    _check(x, f"handed over, {mode}", **kw)
 
 
 def test_status_rows_and_padding():

@@ -117,6 +117,32 @@ def test_spiked_rows():
         _check(x, f"spikes P {P}", temperature=0.7, top_p=P, uniforms=_u(B, g))
 
 
+@pytest.mark.parametrize("mode", ["penalty", "mask", "mask + penalty"])
+def test_rows_handed_over_in_every_variant(mode):
+    """Each variant's rows outside the kernel's bounds run the row-wise path
+    inside the same launch: |y| >= 2^15, a top list beyond its capacity, a
+    NaN (the row-wise path writes the status); the other rows stay on the
+    fp32 top-p path."""
+    B, V = 6, 131072
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(B, V, generator=g) * 2.5
+    x[1, 1000] = 3.0e4
+    x[2, torch.randperm(V, generator=g)[:700]] += 25.0
+    x[3, 5] = float("nan")
+    kw = dict(temperature=0.7, top_p=0.9, uniforms=_u(B, g))
+    if "mask" in mode:
+        bits = torch.rand(B, V, generator=g) < 0.5
+        bits[1, 1000] = True
+        bits[3, 5] = True
+        kw["allow_mask"] = W.pack_mask(bits)
+    if "penalty" in mode:
+        hist = torch.randint(0, V, (B, 2000), generator=g, dtype=torch.int32)
+        hist[1, 0] = 1000
+        kw.update(history=hist, repetition_penalty=1.2)
+    got, _ = _check(x, f"handed over, {mode}", **kw)
+    assert int(got.status[3]) == ops.ROW_NONFINITE
+
+
 @pytest.mark.parametrize("T,P", [(1.0, 0.9), (1.0, 0.95), (1.7, 0.99)])
 def test_large_kept_sets(T, P):
     """Kept sets of 10^4 tokens and more: beyond the candidate array the row
