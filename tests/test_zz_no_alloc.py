@@ -98,3 +98,30 @@ def test_noalloc_rejects_a_call_beyond_its_array():
                                    ctypes.byref(p), None, 0, ids.data_ptr(), None, None, None,
                                    None, None, None, _capi.stream_handle())
     assert rc == 2
+
+
+def test_noalloc_top_p_calls_that_need_no_workspace():
+    """Top-p calls on the one-workgroup kernels need no workspace (a row
+    outside their bounds runs the row-wise path inside the same launch): the
+    allocation-free entry point passes none, and its answers equal those of
+    gtp_sample_rows called without one, a row that takes the in-kernel
+    fallback included."""
+    from tests import _capi
+
+    L = _capi.lib()
+    dev = torch.device("cuda:0")
+    cases = [
+        (96, 70000, torch.bfloat16, dict(temperature=0.8, top_p=0.9), 4),  # > 64 rows: one workgroup per row
+        (8, 70000, torch.float32, dict(temperature=0.7, top_p=0.9), 5),    # fp32 top-p kernel
+    ]
+    for i, (B, V, dtype, params, seed) in enumerate(cases):
+        x, kw = _case(B, V, dtype, params, seed, dev)
+        x[1, 7] = float("-inf") if dtype == torch.bfloat16 else 3.0e4  # the in-kernel fallback
+        _, p, _ = _capi.sample_args(x, **kw)
+        assert L.gtp_sample_workspace_bytes(_capi.DTYPE[dtype], B, V, ctypes.byref(p)) == 0
+        print(f"noalloc top-p call {i}: B={B} V={V} {dtype} {params}", flush=True)
+        rc_w, want = _run(L, "workspace", x, kw, None, 0)
+        rc_n, got = _run(L, "noalloc", x, kw)
+        assert rc_w == 0 and rc_n == 0
+        _same(got, want, f"top-p call {i}")
+        assert (got["status"].numpy() == 0).all()
