@@ -193,8 +193,9 @@ int gtp_sample_route(int dtype, int64_t B, int64_t V, int aligned, int64_t hist_
  * bit-exact outputs).  The workspace is a device array of
  * GTP_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
  * process ends; the first call on a device looks up that device's copy.
- * Each call first clears the array's per-row counters with a small fill
- * kernel on `stream`.  bf16 top-p calls of small batches, whose split rows
+ * Each call that uses the array first clears its per-row counters with a
+ * small fill kernel on `stream` (calls that need no workspace, such as
+ * top-p rows on the one-workgroup kernels, use none).  bf16 top-p calls of small batches, whose split rows
  * would need more, split their rows over fewer workgroups (or none) to fit.
  * Returns GTP_ERR_UNSUPPORTED when any other call needs more than
  * GTP_NOALLOC_SCRATCH_BYTES (gtp_sample_workspace_bytes() tells), e.g.
